@@ -1,0 +1,230 @@
+"""Benchmark of the bfp16-weight GEMM path on one MI355X.
+
+Workload (one step): the DiT FFN pair at M = 4352 tokens, hidden 3072, FF 12288 with bfp16 weights ~N(0, 0.02) and
+bf16 activations ~N(0, 1), seed 0:
+  quantize  x (4352 x 3072 bf16) -> bfp16 packed bytes + decoded bf16 (bit-exact to the CPU packer)
+  up GEMM   4352 x 3072 x (2 x 12288), SwiGLU on the [gate 64 | proj 64] interleave, output re-quantized to bfp16
+  down GEMM 4352 x 12288 x 3072, out = residual + gate[n] * acc
+The metric is the step's GEMM throughput (2MNK summed over both GEMMs, quantize time included) in TFLOP/s. The
+roofline object is for the dominant kernel, the up GEMM (657.13 GFLOP per launch), against the dense bf16 MFMA peak.
+Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
+rotating weight copies so that the 256 MB MALL cannot hold them, and the CPU baseline (the oracle's numpy restatement
+of the reference CPU path on a row sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "redline-tiny_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (vendor figure)
+PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+M, K, FF = 4352, 3072, 12288
+GEMV_K, GEMV_N = 3072, 18432
+
+
+def flops_up():
+    return 2.0 * M * K * 2 * FF
+
+
+def flops_down():
+    return 2.0 * M * FF * K
+
+
+def make_inputs(dev):
+    import numpy as np
+    import torch
+
+    from rlbfp import ops
+
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((M, K), dtype=np.float32)                      # activations first
+    w_gate = rng.standard_normal((FF, K), dtype=np.float32) * 0.02         # then weights
+    w_proj = rng.standard_normal((FF, K), dtype=np.float32) * 0.02
+    w_down = rng.standard_normal((K, FF), dtype=np.float32) * 0.02
+    res = rng.standard_normal((M, K), dtype=np.float32)                    # then epilogue vectors
+    gate = rng.standard_normal(K, dtype=np.float32)
+    t = lambda a, dt: torch.from_numpy(a).to(dev).to(dt)
+    up = ops.pack_weight(ops.interleave_up(t(w_gate, torch.float32), t(w_proj, torch.float32)).contiguous())
+    down = ops.pack_weight(t(w_down, torch.float32))
+    return {"x": t(x, torch.bfloat16), "up": up, "down": down, "res": t(res, torch.bfloat16),
+            "gate": t(gate, torch.float32)}, (x, w_gate, w_proj, w_down, res, gate)
+
+
+class Timer:
+    """HIP events on torch's current stream (the stream the kernels are launched on) around each kernel."""
+
+    def __init__(self):
+        import torch
+        self.torch = torch
+        self.ev = {}
+
+    def mark(self, name):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.ev.setdefault(name, []).append(e)
+
+    def avg_ms(self, a, b):
+        ts = [x.elapsed_time(y) for x, y in zip(self.ev[a], self.ev[b])]
+        return sum(ts) / len(ts)
+
+
+def gpu_bench(steps, warmup):
+    import torch
+
+    from rlbfp import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp, host = make_inputs(dev)
+    h = torch.empty((M, FF), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    xq = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    xp = torch.empty(M * K // 8 * 9, dtype=torch.uint8, device=dev)
+    from rlbfp import _lib as L
+    import ctypes
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def quantize():
+        L.check(L.lib().rl_bfp16_quantize(ctypes.c_void_p(inp["x"].data_ptr()), L.RL_DTYPE_BF16, M, K, K,
+                                          L.RL_ORDER_ROWBLOCK, ctypes.c_void_p(xp.data_ptr()),
+                                          ctypes.c_void_p(xq.data_ptr()), stream()))
+
+    def step(tm=None):
+        if tm:
+            tm.mark("q0")
+        quantize()
+        if tm:
+            tm.mark("up0")
+        ops.gemm(xq, inp["up"], 2 * FF, K, act="swiglu", quantize_out=True, out=h)
+        if tm:
+            tm.mark("down0")
+        ops.gemm(h, inp["down"], K, FF, gate=inp["gate"], residual=inp["res"], out=y)
+        if tm:
+            tm.mark("end")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    tm = Timer()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(tm)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_q, ms_up, ms_down = tm.avg_ms("q0", "up0"), tm.avg_ms("up0", "down0"), tm.avg_ms("down0", "end")
+
+    # GEMV: M = 1 adaLN modulation, weights rotated over 6 copies (382 MB > 256 MB MALL)
+    rng_x = torch.randn((1, GEMV_K), generator=torch.Generator().manual_seed(0)).to(dev, torch.bfloat16)
+    copies = []
+    for c in range(6):
+        g = torch.Generator(device=dev).manual_seed(100 + c)
+        copies.append(ops.pack_weight(torch.randn((GEMV_N, GEMV_K), generator=g, device=dev) * 0.02))
+    ym = torch.empty((1, GEMV_N), dtype=torch.bfloat16, device=dev)
+    for i in range(12):
+        ops.gemv(rng_x, copies[i % 6], GEMV_N, out=ym)
+    torch.cuda.synchronize()
+    n_gemv = 240
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n_gemv):
+        ops.gemv(rng_x, copies[i % 6], GEMV_N, out=ym)
+    e1.record()
+    torch.cuda.synchronize()
+    us_gemv = e0.elapsed_time(e1) * 1e3 / n_gemv
+    gemv_bytes = GEMV_K * GEMV_N * 9 / 8 + GEMV_K * 2 + GEMV_N * 2
+    return {
+        "host": host, "p_up": inp["up"].cpu().numpy(), "p_down": inp["down"].cpu().numpy(),
+        "wall_s": wall, "ms_q": ms_q, "ms_up": ms_up, "ms_down": ms_down, "us_gemv": us_gemv,
+        "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
+    }
+
+
+def cpu_baseline(host, p_up, p_down, rows=1024):
+    """The oracle's numpy restatement of the reference CPU path on the first `rows` rows of the same workload:
+    to_bfp16 of the activations, from_bfp16 of the activations and of the pre-packed weights (the same bytes the GPU
+    uses; packing is an offline cost and is not timed), float32 BLAS matmul, SwiGLU, bf16 rounding, re-quantize,
+    down matmul, gate * acc + residual, bf16 rounding."""
+    import numpy as np
+
+    from oracle import bfp16 as F
+
+    x, _wg, _wp, _wd, res, gate = host
+    x = F.bf16_round(x[:rows])
+    res = F.bf16_round(res[:rows])
+    t0 = time.perf_counter()
+    xq = F.quantize_rows(x)
+    acc = xq @ F.decode_b(p_up, K, 2 * FF)
+    gt = acc.reshape(rows, -1, 2, 64)
+    hv = gt[:, :, 0] / (1 + np.exp(-gt[:, :, 0])) * gt[:, :, 1]
+    hq = F.quantize_rows(F.bf16_round(hv.reshape(rows, FF).astype(np.float32)))
+    out = F.bf16_round((res + gate * (hq @ F.decode_b(p_down, FF, K))).astype(np.float32))
+    dt = time.perf_counter() - t0
+    assert out.shape == (rows, K)
+    flops = 2.0 * rows * K * 2 * FF + 2.0 * rows * FF * K
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads") or 0) for i in threadpool_info()) or None
+    except Exception:
+        pass
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads or len(os.sched_getaffinity(0)), "kind": "port",
+            "sample": f"rows 0..{rows - 1} of the {M}-row FFN pair with the full weights decoded, {dt:.2f} s; numpy "
+                      f"float32 BLAS, {len(os.sched_getaffinity(0))} host cpus visible"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by weight columns, "
+              "see DESIGN.md, but multi-GPU runs are not part of this build)", file=sys.stderr)
+        sys.exit(2)
+    r = gpu_bench(args.steps, args.warmup)
+    ms_step = r["wall_s"] * 1e3 / args.steps
+    step_flops = flops_up() + flops_down()
+    up_tflops = flops_up() / (r["ms_up"] * 1e-3) / 1e12
+    line = {
+        "metric": "bfp16-weight GEMM TFLOP/s and % bf16 MFMA peak at DiT FFN shape; GEMV GB/s",
+        "value": round(step_flops / (ms_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "dit_ffn_pair", "M": M, "hidden": K, "ff": FF,
+                   "step": "quantize x + up GEMM (SwiGLU, re-quantized H) + down GEMM (gate*acc + residual)",
+                   "weights": "bfp16ebs8 ~N(0,0.02)", "activations": "bf16 ~N(0,1)", "seed": 0},
+        "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(up_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_kernel<bf16> up GEMM 4352x3072x24576 + SwiGLU", "us": round(r["ms_up"] * 1e3, 2)},
+        "kernels": {
+            "quantize_us": round(r["ms_q"] * 1e3, 2),
+            "quantize_gbps": round(M * K * (2 + 9 / 8 + 2) / (r["ms_q"] * 1e-3) / 1e9, 1),
+            "up_us": round(r["ms_up"] * 1e3, 2), "up_tflops": round(up_tflops, 2),
+            "down_us": round(r["ms_down"] * 1e3, 2),
+            "down_tflops": round(flops_down() / (r["ms_down"] * 1e-3) / 1e12, 2),
+        },
+        "gemv": {"shape": [1, GEMV_K, GEMV_N], "us": round(r["us_gemv"], 2), "gbps": round(r["gemv_gbps"], 1),
+                 "frac_hbm": round(r["gemv_gbps"] / PEAK_HBM_GBPS, 4), "bytes": int(r["gemv_bytes"]),
+                 "copies": 6},
+    }
+    line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(r["host"], r["p_up"], r["p_down"])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

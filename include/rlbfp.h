@@ -1,0 +1,145 @@
+/* rlbfp.h: C ABI of the MI355X (gfx950) bfp16-weight GEMM path.
+ *
+ * Format "bfp16ebs8": a block is 8 consecutive values stored in 9 bytes [E][q0..q7]; value = q_i * 2^(E-133), E =
+ * the block's largest float32 exponent field, q_i = clip(rint(x_i * 2^(133-E)), -128, 127), round half to even
+ * (redline/npu_layouts.py:62-73, :90-94). Blocks run along K for both GEMM operands.
+ *
+ * Conventions for every entry point:
+ *   - pointers are device pointers (HIP global memory) unless stated; sizes are int64 element counts;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); work is enqueued, never synchronised;
+ *   - outputs are caller-allocated; no entry point allocates device memory (GEMV scratch is passed in);
+ *   - the return value is RL_OK (0) or an RL_ERR_* code; rl_last_error() gives a message for the calling thread.
+ * The reference's interfaces are Python (numpy host code and NPU artifacts run through XRT); each declaration cites
+ * the reference function it replaces.
+ */
+#ifndef RLBFP_H
+#define RLBFP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------------------------------------- */
+enum {
+  RL_OK = 0,
+  RL_ERR_NULL = 1,      /* a required pointer is NULL */
+  RL_ERR_SHAPE = 2,     /* a size is not a multiple the layout needs, or is out of range */
+  RL_ERR_ARG = 3,       /* an enum or flag value is unknown, or arguments contradict each other */
+  RL_ERR_ALIGN = 4,     /* a pointer or leading dimension breaks the kernel's alignment */
+  RL_ERR_DEVICE = 5,    /* the current device is not gfx950, or a HIP call failed */
+  RL_ERR_WORKSPACE = 6  /* the scratch buffer passed in is too small */
+};
+
+/* ---- element types ---------------------------------------------------------------------------------------------- */
+enum { RL_DTYPE_F32 = 0, RL_DTYPE_BF16 = 1 };
+
+/* ---- block orders of a packed stream ---------------------------------------------------------------------------
+ * For an (R, C) matrix with blocks of 8 consecutive columns of a row, unless stated.                              */
+enum {
+  RL_ORDER_ROWBLOCK = 0, /* row major: block (r, c/8) at index r*(C/8) + c/8, i.e. to_bfp16(x.reshape(-1))          */
+  RL_ORDER_A_LAYOUT = 1, /* to_bfp16(a_layout(x, 128, 64)), npu_layouts.py:18-22; R%128 == 0, C%64 == 0             */
+  RL_ORDER_B_LAYOUT = 2, /* x is a Linear weight W (N=R rows, K=C cols); to_bfp16(b_layout(W.T, 64, 128)),
+                            npu_layouts.py:11-15 and pack_weights.py:72-79; R%128 == 0, C%64 == 0                  */
+  RL_ORDER_C_ATB = 3     /* to_bfp16(c_layout_atb(x, 128, 128)), npu_layouts.py:42-47; R%512 == 0, C%1024 == 0      */
+};
+
+/* Encode an (rows, cols) row-major matrix (leading dimension ld_x elements) to bfp16, bit-exact to the CPU packer.
+ * packed: 9*rows*cols/8 bytes in `order` (may be NULL); deq: the decoded values as bf16, row major rows x cols
+ * (may be NULL; the exact bfp16 values, consumed directly by rl_bfp16_gemm with RL_A_BF16). cols % 8 == 0.
+ * Replaces npu_layouts.to_bfp16 (redline/npu_layouts.py:62-73) composed with a_layout / b_layout / c_layout_atb
+ * (:11-22, :42-47), and pack_weights.pack_b (redline/pack_weights.py:72-79) for order RL_ORDER_B_LAYOUT. */
+int rl_bfp16_quantize(const void *x, int32_t x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int32_t order,
+                      uint8_t *packed, uint16_t *deq, void *stream);
+
+/* Decode a packed stream in `order` back to an (rows, cols) row-major matrix of out_dtype (exact).
+ * Replaces npu_layouts.from_bfp16 (redline/npu_layouts.py:90-94) composed with a_unlayout / b_unlayout /
+ * c_unlayout_atb (:56-59, :50-53, :31-39). For RL_ORDER_B_LAYOUT the output is W (N rows, K cols). */
+int rl_bfp16_dequantize(const uint8_t *packed, int32_t order, int64_t rows, int64_t cols, void *out,
+                        int32_t out_dtype, void *stream);
+
+/* ---- GEMM -------------------------------------------------------------------------------------------------------
+ * C = epilogue(A @ B), A (M, K), B (K, N) packed in b_layout(64, 128) order (the bytes pack_weights.py writes),
+ * fp32 accumulation on bf16 MFMA, bf16 output. M >= 1, N % 128 == 0, K % 64 == 0.                                  */
+enum {
+  RL_A_BF16 = 0,          /* bf16 row major, used as is (already bfp16 values, e.g. rl_bfp16_quantize's deq)  */
+  RL_A_BF16_QUANTIZE = 1, /* bf16 row major, quantized to bfp16 along K while it is loaded                     */
+  RL_A_PACKED_ROWBLOCK = 2, /* packed, RL_ORDER_ROWBLOCK of (M, K); lda ignored                                   */
+  RL_A_PACKED_A_LAYOUT = 3  /* packed, RL_ORDER_A_LAYOUT of (M, K) (the NPU's A operand); M%128 == 0; lda ignored */
+};
+enum {
+  RL_ACT_NONE = 0,
+  RL_ACT_GELU_TANH = 1, /* x * sigmoid(2u), u = sqrt(2/pi)(x + 0.044715 x^3) (kernels/vlm/gelu_bfp.cc:1-8)        */
+  RL_ACT_SWIGLU = 2     /* B columns interleaved [gate 64 | proj 64] per 128 (pack_weights.py:82-89): output (M, N/2),
+                           out[:, 64t+u] = silu(v[:, 128t+u]) * v[:, 128t+64+u] (kernels/atb3/mm_bfp_swiglu.cc)  */
+};
+enum {
+  RL_EP_QUANTIZE_OUT = 1 /* after the bf16 rounding, re-quantize each 8-column block of the output to bfp16 (the
+                            stored bf16 values are then exact bfp16 values, ready as the next GEMM's RL_A_BF16)    */
+};
+
+/* Fused epilogue, applied in fp32 in this order: v = acc + bias[n]; v = act(v); v = residual[m][n] + g[n] * v with
+ * g = gate row 1 for rows < gate_split_row else gate row 0 (gate NULL = 1); out = bf16(v) (RNE); optional
+ * re-quantize. The gate/residual step is the adaLN "x' = x + g * branch" (redline/run_ln.py:65-67, rows_param
+ * :82-86; kernels/glue/ln_mod.cc:92-143) fused into the producing GEMM. n indexes output columns. */
+typedef struct rl_epilogue {
+  int32_t act;               /* RL_ACT_* */
+  int32_t flags;             /* RL_EP_* */
+  const float *bias;         /* [N] (pre-activation, all computed columns) or NULL */
+  const float *gate;         /* [Nout] or [2][Nout] (row 1 used for rows < gate_split_row) or NULL */
+  int64_t gate_split_row;    /* 0 = every row uses gate row 0 */
+  const uint16_t *residual;  /* bf16 (M, Nout) with leading dimension ld_residual, or NULL */
+  int64_t ld_residual;
+} rl_epilogue;
+
+/* One GEMM. lda / ldc in elements (bf16); ldc >= Nout (N, or N/2 for SwiGLU). ep may be NULL (plain bf16 C).
+ * Replaces forward.gemm / NPU.run(op, GEMMS[op, M], [A, B, C]) (redline/forward.py:194-197, :138-165), the ATB
+ * microkernels matmul_vectorized_bfp16 (kernels/atb3/mm_bfp_mixed.cc:61, mm_bfp_rho.cc:64, vlm/mm_bfp_c16.cc:62)
+ * and, with RL_ACT_SWIGLU, matmul_swiglu_bfp16 (kernels/atb3/mm_bfp_swiglu.cc:88). */
+int rl_bfp16_gemm(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *stream);
+
+/* Several independent GEMMs (different shapes, weights and epilogues, one A format) in one launch, e.g. the image-
+ * and text-stream projections of a DiT block. At most RL_MAX_GROUP descriptors. Replaces the per-op sequence of
+ * CachedStep.blocks (redline/forward.py:240-254) for GEMMs that do not depend on each other. */
+#define RL_MAX_GROUP 16
+typedef struct rl_gemm_desc {
+  const void *A;
+  int64_t lda;
+  const uint8_t *B_packed;
+  uint16_t *C;
+  int64_t ldc;
+  int64_t M, N, K;
+  rl_epilogue ep;
+} rl_gemm_desc;
+int rl_bfp16_gemm_grouped(const rl_gemm_desc *descs, int32_t n, int32_t a_fmt, void *stream);
+
+/* ---- GEMV (adaLN modulation) -------------------------------------------------------------------------------------
+ * y (M, N) bf16 = act(x) @ B, x (M, K) bf16 with leading dimension ldx, B packed in b_layout(64, 128) order,
+ * 1 <= M <= 8, N % 16 == 0 (and N % 128 == 0 for the layout), K % 64 == 0; act = RL_ACT_NONE or RL_GEMV_SILU;
+ * fp32 accumulation; x is not quantized. Replaces host_glue.modulation / linear(silu(te), W)
+ * (redline/host_glue.py:22-28, :43-48), which the reference runs in numpy float32 on the host. */
+enum { RL_GEMV_SILU = 3 };
+int rl_bfp16_gemv(const uint16_t *x, int64_t ldx, const uint8_t *B_packed, uint16_t *y, int64_t ldy, int64_t M,
+                  int64_t N, int64_t K, int32_t act, void *stream);
+
+/* ---- host-only helpers (no GPU needed) ---------------------------------------------------------------------------- */
+/* Shape/argument checks the entry points run before launching, callable on a machine without a GPU. */
+int rl_validate_quantize(int32_t x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int32_t order);
+int rl_validate_gemm(int32_t a_fmt, int64_t lda, int64_t ldc, int64_t M, int64_t N, int64_t K, const rl_epilogue *ep);
+int rl_validate_gemv(int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t act);
+/* Bytes of a packed stream holding rows x cols values (9 per 8). */
+int64_t rl_packed_bytes(int64_t rows, int64_t cols);
+/* Message for the last error on the calling thread ("" after success). */
+const char *rl_last_error(void);
+/* Library version string. */
+const char *rl_version(void);
+/* RL_OK when the current HIP device is a gfx950 (MI355X); RL_ERR_DEVICE otherwise. Initialises HIP. */
+int rl_device_check(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLBFP_H */

@@ -1,0 +1,531 @@
+// bfp16-weight GEMM for gfx950: C = epilogue(A @ B), B streamed from HBM in the packed b_layout(64, 128) order that
+// redline/pack_weights.py:72-79 writes, decoded to bf16 in registers, bf16 MFMA with fp32 accumulation.
+//
+// Replaces the ATB microkernels (kernels/atb3/mm_bfp_mixed.cc:61, mm_bfp_rho.cc:64, kernels/vlm/mm_bfp_c16.cc:62)
+// and the SwiGLU-flush GEMM (kernels/atb3/mm_bfp_swiglu.cc:88) behind forward.gemm / NPU.run (redline/forward.py).
+//
+// Tiling (one 256x256 output tile per workgroup, 4 waves, K steps of 64):
+//   * wave w owns four 16-column groups of the tile and all 256 rows: 16 x 4 MFMA 16x16x32 accumulators (256 fp32
+//     per lane). Its groups are 4w..4w+3, or for SwiGLU the gate groups {g, g+1} and proj groups {g+4, g+5} of one
+//     128-column tile, so silu(gate) * proj pairs sit in the same lane and register.
+//   * B never touches LDS: in the b_layout a 16-column group x 32 K is 64 consecutive 9-byte blocks (576 bytes),
+//     and lane l's MFMA operand (column l%16, K 8(l/16)..+7) is exactly block l. Each lane reads its block through a
+//     dword-aligned 12-byte window and decodes it (sign-extending byte converts, one scale multiply, bf16 packing).
+//     Every B element is decoded once per workgroup.
+//   * A (bf16, row major) is staged through a double-buffered LDS tile (256 x 64 bf16 = 32 KB per stage) with a
+//     16-byte-chunk XOR swizzle; all four waves read it as ds_read_b128 operands.
+//   * loads run two K steps ahead: while the MFMAs of step k run, the raw B windows and the A chunks of step k+1
+//     are in flight; after them B(k+1) is decoded and A(k+1) stored to the other LDS stage.
+//   * workgroups are remapped so each XCD walks a contiguous range of tiles, grouped 8 M-tiles at a time.
+#include <stdio.h>
+
+#include "rlbfp.h"
+#include "rlbfp_device.h"
+#include "rlbfp_host.h"
+
+namespace rl {
+
+constexpr int BM = 256, BN = 256, BK = 64;
+constexpr int kGThreads = 256;
+constexpr int kAStage = BM * BK * 2;  // bytes of one A stage
+constexpr int kTileBytes = 64 * 128 * 9 / 8;  // one b_layout tile (64 K x 128 N)
+constexpr int kGroupM = 8;
+
+struct GemmDesc {
+  const void* A;
+  int64_t lda;
+  const uint8_t* B;
+  uint16_t* C;
+  int64_t ldc;
+  int32_t M, N, K;
+  int32_t act, flags;
+  int32_t gate_split;
+  const float* bias;
+  const float* gate;
+  const uint16_t* res;
+  int64_t ldr;
+  int32_t tiles_m, tiles_n, tile_start, pad_;
+};
+
+template <int G>
+struct GemmArgs {
+  GemmDesc d[G];
+  int32_t n;
+};
+
+// Waits until at most N vector-memory loads of this wave are outstanding (s_waitcnt vmcnt(N), gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// 16-byte chunk swizzle of the A tile: chunk c of row r is stored at chunk c ^ swz(r). A wave's ds_read_b128 of one
+// chunk column over 16 consecutive rows then spreads over all banks.
+__device__ __forceinline__ int a_swz(int r) { return (r >> 1) & 7; }
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float gelu_tanh_f(float x) {
+  // x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
+  const float u2 = 1.5957691216057308f * (x + 0.044715f * x * x * x);
+  return x / (1.0f + __expf(-u2));
+}
+
+// float32 -> bf16 bits, round half to even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_rne(float v) {
+  const uint32_t u = __float_as_uint(v);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// max over the 8 lanes of each aligned 8-lane group (DPP: quad xor 1, quad xor 2, half-row mirror).
+__device__ __forceinline__ uint32_t max8(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));
+  return x;
+}
+
+// bf16 value (as bits) re-quantized to bfp16 with the block exponent shared by its 8-lane group, returned as bits.
+// Exact: the scaling is by powers of two and rint is half-to-even; -0 is returned as +0 like from_bfp16.
+__device__ __forceinline__ uint32_t requantize_bits(uint32_t b) {
+  const uint32_t E = max8((b >> 7) & 0xFFu);
+  const float v = __uint_as_float(b << 16);
+  float q = __builtin_rintf(__builtin_amdgcn_ldexpf(v, 133 - (int)E));
+  q = fminf(q, 127.0f);
+  const float d = __builtin_amdgcn_ldexpf(q, (int)E - 133) + 0.0f;
+  return __float_as_uint(d) >> 16;
+}
+
+constexpr int kEPitch = BN + 4;  // floats per row of the epilogue tile (the pad spreads 4 row groups over banks)
+static_assert(64 * kEPitch * 4 <= 3 * kAStage, "epilogue tile must fit the LDS allocation");
+
+// 8 values of one output block: bias, activation, gate / residual, bf16 rounding (RNE) and the optional bfp16
+// re-quantize, all in fp32; returns the 8 bf16 as 4 words.
+__device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int ocol, int nout, float (&v)[8]) {
+  if (d.gate || d.res) {
+    const float* g = d.gate ? d.gate + (row < d.gate_split ? nout : 0) + ocol : nullptr;
+    u32x4 r = {0u, 0u, 0u, 0u};
+    if (d.res) r = *reinterpret_cast<const u32x4*>(d.res + (int64_t)row * d.ldr + ocol);
+    const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float gk = g ? g[k] : 1.0f;
+      const float rk = __uint_as_float(k & 1 ? rw[k >> 1] & 0xFFFF0000u : rw[k >> 1] << 16);
+      v[k] = rk + gk * v[k];
+    }
+  }
+  uint32_t b[8];
+#pragma unroll
+  for (int k = 0; k < 8; k++) b[k] = bf16_rne(v[k]);
+  u32x4 o = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+  if (d.flags & RL_EP_QUANTIZE_OUT) o = quantize_bf16x8(o);
+  return o;
+}
+
+// Phase B of the epilogue for 64 rows starting at r0: the LDS tile holds the fp32 accumulators of computed columns
+// n0..n0+255 (row pitch kEPitch).
+__device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep, int r0, int n0, int nout, int tid) {
+  if (d.act == RL_ACT_SWIGLU) {
+    // 64 rows x 128 output columns = 1024 blocks; block b: row b / 16, output block b % 16 of this tile
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+      const int b = it * kGThreads + tid;
+      const int rr = b >> 4, ob = b & 15;
+      const int gc = (ob >> 3) * 128 + (ob & 7) * 8;  // gate column in the tile; proj = gc + 64
+      const int row = r0 + rr;
+      if (row >= d.M || n0 + gc >= d.N) continue;
+      const float* src = ep + rr * kEPitch + gc;
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(src), g1 = *reinterpret_cast<const f32x4*>(src + 4);
+      const f32x4 p0 = *reinterpret_cast<const f32x4*>(src + 64), p1 = *reinterpret_cast<const f32x4*>(src + 68);
+      float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+      if (d.bias) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          gv[k] += d.bias[n0 + gc + k];
+          pv[k] += d.bias[n0 + gc + 64 + k];
+        }
+      }
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = silu_f(gv[k]) * pv[k];
+      const int ocol = ((n0 + gc) >> 1) + 0;  // 64t + u with t = col / 128, u = col % 64 (gc % 128 < 64)
+      const u32x4 o = finish_block(d, row, ocol, nout, v);
+      *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
+    }
+  } else {
+    // 64 rows x 256 columns = 2048 blocks; block b: row b / 32, column block b % 32
+#pragma unroll
+    for (int it = 0; it < 8; it++) {
+      const int b = it * kGThreads + tid;
+      const int rr = b >> 5, cb = b & 31;
+      const int row = r0 + rr, col = n0 + cb * 8;
+      if (row >= d.M || col >= d.N) continue;
+      const float* src = ep + rr * kEPitch + cb * 8;
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(src), a1 = *reinterpret_cast<const f32x4*>(src + 4);
+      float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      if (d.bias) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] += d.bias[col + k];
+      }
+      if (d.act == RL_ACT_GELU_TANH) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = gelu_tanh_f(v[k]);
+      }
+      const u32x4 o = finish_block(d, row, col, nout, v);
+      *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
+    }
+  }
+}
+
+// Loads this thread's eight 16-byte A chunks of K step kt: rows (tid>>3) + 32i, chunk tid&7.
+template <int AFMT>
+__device__ __forceinline__ void load_a(const GemmDesc& d, int m0, int kt, int tid, u32x4 (&av)[8]) {
+  const int c = tid & 7;
+  const int KB = d.K >> 3;  // K blocks per row
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int r = min(m0 + (tid >> 3) + 32 * i, d.M - 1);
+    if constexpr (AFMT == RL_A_BF16 || AFMT == RL_A_BF16_QUANTIZE) {
+      const uint16_t* p = static_cast<const uint16_t*>(d.A) + (int64_t)r * d.lda + kt * BK + c * 8;
+      av[i] = *reinterpret_cast<const u32x4*>(p);
+    } else {
+      int64_t blk;
+      const int kb = kt * 8 + c;
+      if constexpr (AFMT == RL_A_PACKED_ROWBLOCK) {
+        blk = (int64_t)r * KB + kb;
+      } else {  // A_LAYOUT: ((((mt*KT + kt)*8 + sbr)*8 + bc)*2 + bis)*8 + rib
+        const int KT = d.K >> 6;
+        blk = ((((((int64_t)(r >> 7) * KT + kt) * 8 + ((r >> 4) & 7)) * 8 + c) * 2 + ((r >> 3) & 1)) * 8) + (r & 7);
+      }
+      const Window w = load_window(static_cast<const uint8_t*>(d.A), blk * 9);
+      av[i] = u32x4{w.w0, w.w1, w.w2, (uint32_t)(blk & 3)};
+    }
+  }
+}
+
+// Converts the loaded A chunks to bf16 MFMA operands and stores them into an LDS stage.
+template <int AFMT>
+__device__ __forceinline__ void store_a(uint8_t* stage, int tid, const u32x4 (&av)[8]) {
+  const int c = tid & 7;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int r = (tid >> 3) + 32 * i;
+    u32x4 v = av[i];
+    if constexpr (AFMT == RL_A_BF16_QUANTIZE) {
+      v = quantize_bf16x8(v);
+    } else if constexpr (AFMT == RL_A_PACKED_ROWBLOCK || AFMT == RL_A_PACKED_A_LAYOUT) {
+      v = __builtin_bit_cast(u32x4, decode_window(v.x, v.y, v.z, v.w));
+    }
+    *reinterpret_cast<u32x4*>(stage + r * (BK * 2) + ((c ^ a_swz(r)) << 4)) = v;
+  }
+}
+
+template <int AFMT, int G>
+__global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> args) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kAStage];
+
+  const int pid = xcd_remap(blockIdx.x, gridDim.x);
+  int di = 0;
+  if constexpr (G > 1) {
+    for (int i = 1; i < args.n; i++)
+      if (pid >= args.d[i].tile_start) di = i;
+  }
+  const GemmDesc& d = args.d[di];
+  const int local = pid - d.tile_start;
+  const int group = local / (kGroupM * d.tiles_n);
+  const int first_m = group * kGroupM;
+  const int gm = min(d.tiles_m - first_m, kGroupM);
+  const int in_group = local - group * kGroupM * d.tiles_n;
+  const int m0 = (first_m + in_group % gm) * BM;
+  const int n0 = (in_group / gm) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int KT = d.K / BK;
+  const int N = d.N;
+
+  // this wave's four 16-column groups
+  int grp[4];
+  if (d.act == RL_ACT_SWIGLU) {
+    const int g = 8 * (wave >> 1) + 2 * (wave & 1);
+    grp[0] = g; grp[1] = g + 1; grp[2] = g + 4; grp[3] = g + 5;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++) grp[j] = 4 * wave + j;
+  }
+  const bool active = n0 + 16 * grp[0] < d.N;  // a wave's groups share one 128-column tile; N % 128 == 0
+
+  // byte offsets of this lane's B windows at K step 0, K half 0; step kt adds kt * 9216, half h adds 576
+  const uint8_t* bptr[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int col = n0 + 16 * grp[j];
+    const int64_t t = active ? (int64_t)(col >> 7) * KT : 0;
+    const int sbc = (col >> 4) & 7;
+    bptr[j] = d.B + ((t * kTileBytes + (int64_t)(sbc * 128 + lane) * 9) & ~(int64_t)3);
+  }
+  const uint32_t bo = lane & 3;  // byte offset of the block inside its window: (9 * lane) % 4
+
+  f32x4 acc[16][4];
+#pragma unroll
+  for (int mf = 0; mf < 16; mf++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[mf][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // A operand read addresses: row 16mf + lane%16, chunk 4h + lane/16 (swizzled); the swizzle depends only on lane
+  const int arow = lane & 15;
+  const int aoff0 = arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
+  const int aoff1 = arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
+
+  bf16x8 bcur[4][2];
+  // MFMAs of one K half (h) of one step over the 16 row fragments, with the A stage at st
+  // (A fragments are read three row fragments ahead of their MFMAs, so that LDS latency hides under MFMAs)
+  auto mfma_half = [&](const uint8_t* st, int aoff, int h) {
+    constexpr int kAhead = 3;
+    bf16x8 a[kAhead];
+#pragma unroll
+    for (int mf = 0; mf < kAhead; mf++) a[mf] = *reinterpret_cast<const bf16x8*>(st + mf * 16 * (BK * 2) + aoff);
+#pragma unroll
+    for (int mf = 0; mf < 16; mf++) {
+      const bf16x8 cur = a[mf % kAhead];
+      if (mf + kAhead < 16)
+        a[mf % kAhead] = *reinterpret_cast<const bf16x8*>(st + (mf + kAhead) * 16 * (BK * 2) + aoff);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, bcur[j][h], acc[mf][j], 0, 0, 0);
+    }
+  };
+
+  if constexpr (AFMT == RL_A_BF16) {
+    // ---- pipelined path: A by direct-to-LDS loads into 3 stages, B windows in 3 register slots, both issued two
+    // steps ahead. Within a step, the B half not being multiplied is decoded under the MFMAs of the other half:
+    // first half (K 0..31 of the step) decodes this step's second half, second half decodes the next step's first.
+    uint32_t raw[3][4][2][3];
+    auto load_raw = [&](uint32_t (&r)[4][2][3], int kt) {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t* p = reinterpret_cast<const uint32_t*>(bptr[j] + (int64_t)kt * kTileBytes + h * 576);
+          r[j][h][0] = p[0];
+          r[j][h][1] = p[1];
+          r[j][h][2] = p[2];
+        }
+    };
+    auto decode_half = [&](const uint32_t (&r)[4][2][3], int h) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) bcur[j][h] = decode_window(r[j][h][0], r[j][h][1], r[j][h][2], bo);
+    };
+    // wave w fills rows 64w..64w+63 of a stage: 8 loads of 8 rows; lane l -> row +l/8, LDS chunk l%8, which holds
+    // logical chunk (l%8) ^ swz(row)
+    const int dma_row = 64 * wave + (lane >> 3);
+    auto dma_a = [&](int stage, int kt) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int r = dma_row + 8 * i;
+        const int c = (lane & 7) ^ a_swz(r);
+        const int gr = min(m0 + r, d.M - 1);
+        const uint16_t* src = static_cast<const uint16_t*>(d.A) + (int64_t)gr * d.lda + kt * BK + c * 8;
+        uint8_t* dst = lds + stage * kAStage + (64 * wave + 8 * i) * (BK * 2);
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+      }
+    };
+
+    // prologue: steps 0 and 1 in flight, step 0's first half decoded
+    dma_a(0, 0);
+    if (active) load_raw(raw[0], 0);
+    if (KT > 1) {
+      dma_a(1, 1);
+      if (active) load_raw(raw[1], 1);
+    }
+    if (active) decode_half(raw[0], 0);
+    wait_vm<0>();
+    __syncthreads();
+
+    auto step = [&]<int S>(int kt) {
+      const bool more = kt + 2 < KT;
+      if (more) {
+        dma_a((S + 2) % 3, kt + 2);
+        if (active) load_raw(raw[(S + 2) % 3], kt + 2);
+      }
+      const uint8_t* st = lds + S * kAStage;
+      if (active) {
+        decode_half(raw[S], 1);
+        mfma_half(st, aoff0, 0);
+        if (kt + 1 < KT) decode_half(raw[(S + 1) % 3], 0);
+        mfma_half(st, aoff1, 1);
+      }
+      // A(kt+1) must have landed before the barrier; the loads issued in this step may stay in flight
+      if (more)
+        wait_vm<16>();
+      else
+        wait_vm<0>();
+      __syncthreads();
+    };
+    int kt = 0;
+    for (; kt + 3 <= KT; kt += 3) {
+      step.template operator()<0>(kt);
+      step.template operator()<1>(kt + 1);
+      step.template operator()<2>(kt + 2);
+    }
+    if (kt < KT) step.template operator()<0>(kt);
+    if (kt + 1 < KT) step.template operator()<1>(kt + 1);
+  } else {
+    // ---- register-staged path (A converted from bf16-with-quantize or packed bytes): B of the next step is loaded
+    // before the MFMAs of this step, A after them; both are converted before the barrier.
+    uint32_t braw[4][2][3];
+    auto load_b = [&](int kt) {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t* p = reinterpret_cast<const uint32_t*>(bptr[j] + (int64_t)kt * kTileBytes + h * 576);
+          braw[j][h][0] = p[0];
+          braw[j][h][1] = p[1];
+          braw[j][h][2] = p[2];
+        }
+    };
+    auto decode_b = [&]() {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) bcur[j][h] = decode_window(braw[j][h][0], braw[j][h][1], braw[j][h][2], bo);
+    };
+    u32x4 av[8];
+    load_a<AFMT>(d, m0, 0, tid, av);
+    if (active) load_b(0);
+    store_a<AFMT>(lds, tid, av);
+    if (active) decode_b();
+    __syncthreads();
+    for (int kt = 0; kt < KT; kt++) {
+      const uint8_t* st = lds + (kt & 1) * kAStage;
+      if (kt + 1 < KT && active) load_b(kt + 1);
+      if (active) {
+        mfma_half(st, aoff0, 0);
+        mfma_half(st, aoff1, 1);
+      }
+      if (kt + 1 < KT) {
+        load_a<AFMT>(d, m0, kt + 1, tid, av);
+        store_a<AFMT>(lds + ((kt + 1) & 1) * kAStage, tid, av);
+        if (active) decode_b();
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- epilogue: through LDS, 64 rows at a time ----------------------------------------------------------------
+  // Phase A: each wave writes its fp32 accumulators for 64 rows into a row-major LDS tile (pitch kEPitch floats).
+  // Phase B: each thread takes one 8-column output block of a row (one bfp16 block when re-quantizing), applies the
+  // epilogue in fp32 and writes 16 bytes of bf16; a wave writes 512 contiguous bytes per row.
+  float* ep = reinterpret_cast<float*>(lds);
+  const int col_in = lane & 15;
+  const int row_in = 4 * (lane >> 4);
+  const bool swiglu = d.act == RL_ACT_SWIGLU;
+  const int nout = swiglu ? N / 2 : N;
+  auto pass = [&]<int P>() {
+    if (active) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int c = 16 * grp[j] + col_in;
+#pragma unroll
+        for (int f = 0; f < 4; f++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) ep[(16 * f + row_in + i) * kEPitch + c] = acc[4 * P + f][j][i];
+      }
+    }
+    __syncthreads();
+    epilogue_rows(d, ep, m0 + 64 * P, n0, nout, tid);
+    __syncthreads();
+  };
+  pass.template operator()<0>();
+  pass.template operator()<1>();
+  pass.template operator()<2>();
+  pass.template operator()<3>();
+}
+
+template <int G>
+static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, uint16_t* C, int64_t ldc, int64_t M,
+                     int64_t N, int64_t K, const rl_epilogue* ep, int32_t a_fmt, int tile_start) {
+  int s = rl_validate_gemm(a_fmt, lda, ldc, M, N, K, ep);
+  if (s) return s;
+  if (!A || !B || !C) return fail(RL_ERR_NULL, "A, B or C is NULL");
+  if ((a_fmt == RL_A_BF16 || a_fmt == RL_A_BF16_QUANTIZE) && ((uintptr_t)A % 16))
+    return fail(RL_ERR_ALIGN, "bf16 A must be 16-byte aligned");
+  if (a_fmt >= RL_A_PACKED_ROWBLOCK && ((uintptr_t)A % 4)) return fail(RL_ERR_ALIGN, "packed A must be 4-byte aligned");
+  if ((uintptr_t)B % 4) return fail(RL_ERR_ALIGN, "B must be 4-byte aligned");
+  if ((uintptr_t)C % 16) return fail(RL_ERR_ALIGN, "C must be 16-byte aligned");
+  if (ep && ep->residual && (((uintptr_t)ep->residual % 16) || ep->ld_residual % 8))
+    return fail(RL_ERR_ALIGN, "residual must be 16-byte aligned with ld_residual %% 8 == 0");
+  if (ep && ep->bias && ((uintptr_t)ep->bias % 4)) return fail(RL_ERR_ALIGN, "bias must be 4-byte aligned");
+  if (ep && ep->gate && ((uintptr_t)ep->gate % 4)) return fail(RL_ERR_ALIGN, "gate must be 4-byte aligned");
+  g.A = A; g.lda = lda; g.B = B; g.C = C; g.ldc = ldc;
+  g.M = (int32_t)M; g.N = (int32_t)N; g.K = (int32_t)K;
+  g.act = ep ? ep->act : RL_ACT_NONE;
+  g.flags = ep ? ep->flags : 0;
+  g.bias = ep ? ep->bias : nullptr;
+  g.gate = ep ? ep->gate : nullptr;
+  g.gate_split = ep ? (int32_t)ep->gate_split_row : 0;
+  g.res = ep ? ep->residual : nullptr;
+  g.ldr = ep ? ep->ld_residual : 0;
+  g.tiles_m = (int32_t)((M + BM - 1) / BM);
+  g.tiles_n = (int32_t)((N + BN - 1) / BN);
+  g.tile_start = tile_start;
+  g.pad_ = 0;
+  return RL_OK;
+}
+
+template <int G>
+static int launch(const GemmArgs<G>& args, int total_tiles, int32_t a_fmt, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(total_tiles), block(kGThreads);
+  switch (a_fmt) {
+    case RL_A_BF16: hipLaunchKernelGGL((gemm_kernel<RL_A_BF16, G>), grid, block, 0, st, args); break;
+    case RL_A_BF16_QUANTIZE: hipLaunchKernelGGL((gemm_kernel<RL_A_BF16_QUANTIZE, G>), grid, block, 0, st, args); break;
+    case RL_A_PACKED_ROWBLOCK:
+      hipLaunchKernelGGL((gemm_kernel<RL_A_PACKED_ROWBLOCK, G>), grid, block, 0, st, args);
+      break;
+    default: hipLaunchKernelGGL((gemm_kernel<RL_A_PACKED_A_LAYOUT, G>), grid, block, 0, st, args); break;
+  }
+  return launch_status("rl_bfp16_gemm");
+}
+
+}  // namespace rl
+
+extern "C" {
+
+int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* stream) {
+  using namespace rl;
+  GemmArgs<1> args;
+  int s = fill_desc<1>(args.d[0], A, lda, B_packed, C, ldc, M, N, K, ep, a_fmt, 0);
+  if (s) return s;
+  args.n = 1;
+  if ((s = check_device())) return s;
+  return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
+}
+
+int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, void* stream) {
+  using namespace rl;
+  if (!descs) return fail(RL_ERR_NULL, "descs is NULL");
+  if (n < 1 || n > RL_MAX_GROUP) return fail(RL_ERR_ARG, "n %d: need 1..%d", n, RL_MAX_GROUP);
+  GemmArgs<RL_MAX_GROUP> args;
+  int total = 0;
+  for (int i = 0; i < n; i++) {
+    const rl_gemm_desc& e = descs[i];
+    int s = fill_desc<RL_MAX_GROUP>(args.d[i], e.A, e.lda, e.B_packed, e.C, e.ldc, e.M, e.N, e.K, &e.ep, a_fmt, total);
+    if (s) {
+      char msg[256];
+      snprintf(msg, sizeof msg, "%s", rl_last_error());
+      return fail(s, "descriptor %d: %s", i, msg);
+    }
+    total += args.d[i].tiles_m * args.d[i].tiles_n;
+  }
+  for (int i = n; i < RL_MAX_GROUP; i++) args.d[i] = args.d[n - 1];
+  args.n = n;
+  int s = check_device();
+  if (s) return s;
+  return launch<RL_MAX_GROUP>(args, total, a_fmt, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,158 @@
+// Device-side helpers shared by the bfp16 kernels (gfx950 / CDNA4, wave64).
+//
+// bfp16ebs8: 8 values in 9 bytes [E][q0..q7], value = q * 2^(E-133), E = the block's largest float32 exponent field,
+// q = clip(rint(x * 2^(133-E)), -128, 127), round half to even (redline/npu_layouts.py:62-73, :90-94).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rl {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlockBytes = 9;
+
+// ---- exact encode: integer arithmetic on the float32 bit pattern -----------------------------------------------
+
+// Largest exponent field of 8 float32 bit patterns.
+__device__ __forceinline__ uint32_t block_exp(const uint32_t u[8]) {
+  uint32_t E = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) E = max(E, (u[i] >> 23) & 0xFFu);
+  return E;
+}
+
+// q for one element given the block exponent E: |x| * 2^(133-E) = m / 2^(E + 17 - e') with m the 24-bit significand
+// (no implicit bit and e' = 1 for subnormals), rounded half to even, signed, clipped to [-128, 127].
+// Infinities saturate (+127 / -128) as np.clip does; NaN is outside the contract.
+__device__ __forceinline__ int32_t encode_elem(uint32_t u, uint32_t E) {
+  const uint32_t e = (u >> 23) & 0xFFu;
+  uint32_t m = u & 0x7FFFFFu;
+  const uint32_t ee = e ? e : 1u;
+  m |= e ? 0x800000u : 0u;
+  const uint32_t s = E + 17u - ee;  // >= 16
+  uint32_t mag = 0;
+  if (s < 32u) {
+    const uint32_t q = m >> s;
+    const uint32_t rem = m & ((1u << s) - 1u);
+    const uint32_t half = 1u << (s - 1u);
+    mag = q + ((rem > half) | ((rem == half) & (q & 1u)));
+  }
+  const bool neg = (u >> 31) != 0;
+  int32_t v = neg ? -(int32_t)mag : (int32_t)mag;
+  if (e == 255u) v = neg ? -128 : 127;
+  return min(v, 127);
+}
+
+// bf16 bit pattern of q * 2^(E-133), built with integers (exact for every E, including bf16 subnormal results).
+// q == 0 gives +0, as from_bfp16 does.
+__device__ __forceinline__ uint32_t decode_bf16_bits(int32_t q, uint32_t E) {
+  if (q == 0) return 0u;
+  const uint32_t sign = q < 0 ? 0x8000u : 0u;
+  const uint32_t a = (uint32_t)(q < 0 ? -q : q);  // 1..128
+  const int p = 31 - __clz(a);                      // leading one, 0..7
+  const int be = p + (int)E - 6;                    // biased exponent of the result
+  uint32_t bits;
+  if (be >= 1)
+    bits = ((uint32_t)be << 7) | ((a << (7 - p)) & 0x7Fu);
+  else
+    bits = a << E;  // subnormal: value / 2^-133
+  return sign | bits;
+}
+
+// ---- fast decode for the GEMM's B operand ---------------------------------------------------------------------
+
+// 2^(E-133) as float (subnormal for E < 7).
+__device__ __forceinline__ float block_scale(uint32_t E) { return __builtin_amdgcn_ldexpf(1.0f, (int)E - 133); }
+
+// Pack the high halves of two float32 (both exactly representable in bf16) into one bf16x2 word: lo | hi << 16.
+__device__ __forceinline__ uint32_t pack_hi(float lo, float hi) {
+  return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// One 9-byte block held in a 12-byte window w0..w2 that starts `o` bytes before it (o = 0..3) -> 8 bf16 values.
+// q bytes are sign-extended to float (one SDWA convert each), scaled by the block exponent, and truncated to bf16
+// (exact: |q| < 2^8 fits bf16's significand).
+__device__ __forceinline__ bf16x8 decode_window(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t o) {
+  const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, o);  // bytes o..o+3: E q0 q1 q2
+  const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, o);  // bytes o+4..o+7: q3 q4 q5 q6
+  const uint32_t q7 = w2 >> (8u * o);                         // byte o+8 in bits 0..7
+  const float s = block_scale(lo & 0xFFu);
+  const float f0 = (float)(int8_t)(lo >> 8) * s;
+  const float f1 = (float)(int8_t)(lo >> 16) * s;
+  const float f2 = (float)(int8_t)(lo >> 24) * s;
+  const float f3 = (float)(int8_t)(hi) * s;
+  const float f4 = (float)(int8_t)(hi >> 8) * s;
+  const float f5 = (float)(int8_t)(hi >> 16) * s;
+  const float f6 = (float)(int8_t)(hi >> 24) * s;
+  const float f7 = (float)(int8_t)(q7) * s;
+  u32x4 r;
+  r.x = pack_hi(f0, f1);
+  r.y = pack_hi(f2, f3);
+  r.z = pack_hi(f4, f5);
+  r.w = pack_hi(f6, f7);
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// Byte address of the 12-byte window holding the 9-byte block at byte offset b9: start rounded down to 4 bytes.
+// For a stream whose block count is a multiple of 8 the window never leaves the stream: a window passes the block's
+// end only when b9 % 4 == 0, i.e. for blocks 0 mod 4, which are never the last block.
+struct Window {
+  uint32_t w0, w1, w2;
+};
+__device__ __forceinline__ Window load_window(const uint8_t* base, int64_t b9) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(base + (b9 & ~(int64_t)3));
+  return Window{p[0], p[1], p[2]};
+}
+
+// Same block, safe for any stream length: a window that would pass the end of a stream of `nblocks` blocks is
+// replaced by byte loads.
+__device__ __forceinline__ Window load_window_safe(const uint8_t* base, int64_t blk, int64_t nblocks) {
+  const int64_t b9 = blk * 9;
+  if ((blk & 3) != 0 || blk + 1 < nblocks) return load_window(base, b9);
+  uint32_t w[3] = {0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 9; i++) w[i >> 2] |= (uint32_t)base[b9 + i] << (8 * (i & 3));
+  return Window{w[0], w[1], w[2]};
+}
+
+// ---- exact quantize of 8 bf16 values (as 4 packed words) to bfp16, returned as bf16 words ----------------------
+__device__ __forceinline__ u32x4 quantize_bf16x8(u32x4 v, uint32_t* E_out = nullptr, int32_t* q_out = nullptr) {
+  uint32_t u[8];
+  u[0] = v.x << 16; u[1] = v.x & 0xFFFF0000u;
+  u[2] = v.y << 16; u[3] = v.y & 0xFFFF0000u;
+  u[4] = v.z << 16; u[5] = v.z & 0xFFFF0000u;
+  u[6] = v.w << 16; u[7] = v.w & 0xFFFF0000u;
+  const uint32_t E = block_exp(u);
+  uint32_t b[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int32_t q = encode_elem(u[i], E);
+    if (q_out) q_out[i] = q;
+    b[i] = decode_bf16_bits(q, E);
+  }
+  if (E_out) *E_out = E;
+  u32x4 r;
+  r.x = b[0] | (b[1] << 16);
+  r.y = b[2] | (b[3] << 16);
+  r.z = b[4] | (b[5] << 16);
+  r.w = b[6] | (b[7] << 16);
+  return r;
+}
+
+// ---- XCD-aware workgroup order -----------------------------------------------------------------------------------
+// Workgroups are dispatched round robin over the 8 XCDs (pid % 8). Map them so that each XCD works on a contiguous
+// range of logical tiles, which then share operands in that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int pid, int nwg) {
+  constexpr int kXcd = 8;
+  const int xcd = pid % kXcd, local = pid / kXcd;
+  const int per = (nwg + kXcd - 1) / kXcd;
+  const int rem = nwg % kXcd;
+  if (rem == 0 || xcd < rem) return xcd * per + local;
+  return rem * per + (xcd - rem) * (per - 1) + local;
+}
+
+}  // namespace rl

@@ -1,0 +1,50 @@
+"""The bfp16 encode/decode names of redline/npu_layouts.py on the HIP kernels (device tensors in, device tensors out).
+
+``to_bfp16(x)`` encodes a flat stream (blocks of 8 consecutive values) and is bit-exact to npu_layouts.to_bfp16
+(redline/npu_layouts.py:62-73, round half to even); ``from_bfp16`` decodes exactly (:90-94). The layout permutations
+are fused into the encoder instead of being separate passes: ``to_bfp16_a_layout`` = to_bfp16(a_layout(x, 128, 64)),
+``pack_b`` = to_bfp16(b_layout(B, 64, 128)) for B = W.T, ``to_bfp16_c_atb`` = to_bfp16(c_layout_atb(x, 128, 128)).
+"""
+
+import torch
+
+from . import ops
+
+
+def to_bfp16(x):
+    """Flat (or any-shaped) float32 / bf16 device tensor, size a multiple of 8 -> packed uint8 stream."""
+    flat = x.reshape(1, -1) if x.numel() < 8 or x.numel() % 8 else x.reshape(-1, 8)
+    p, _ = ops.quantize(flat.contiguous())
+    return p
+
+
+def from_bfp16(raw):
+    """Packed uint8 stream -> flat float32 values."""
+    n = raw.numel() // 9 * 8
+    return ops.dequantize(raw, n // 8, 8).reshape(-1)
+
+
+def to_bfp16_a_layout(x):
+    return ops.quantize(x.contiguous(), order="a_layout")[0]
+
+
+def to_bfp16_c_atb(x):
+    return ops.quantize(x.contiguous(), order="c_atb")[0]
+
+
+def pack_b(B):
+    """(K, N) matrix B = W.T -> packed B stream (redline/pack_weights.py:72-79); pass W (N, K) to pack_weight."""
+    return ops.pack_weight(B.t().contiguous())
+
+
+def from_bfp16_a_layout(raw, M, K):
+    return ops.dequantize(raw, M, K, order="a_layout")
+
+
+def from_bfp16_c_atb(raw, M, N):
+    return ops.dequantize(raw, M, N, order="c_atb")
+
+
+def unpack_b(raw, K, N):
+    """Packed B stream -> the decoded (K, N) matrix."""
+    return ops.dequantize(raw, N, K, order="b_layout").t()

@@ -1,0 +1,213 @@
+"""Tensor-level entry points over librlbfp: quantize / dequantize, the packed-weight GEMM with its fused epilogues,
+grouped GEMMs and the GEMV. Inputs are torch tensors on a ROCm device (gfx950); outputs are allocated here with
+torch's caching allocator (or passed in) and the work is enqueued on torch's current stream.
+
+Packed streams are uint8 tensors of 9 bytes per 8 values. Packed weights are the bytes redline/pack_weights.py writes:
+to_bfp16(b_layout(W.T, 64, 128)) of a Linear weight W (N, K).
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib as L
+
+ORDERS = {"rowblock": L.RL_ORDER_ROWBLOCK, "a_layout": L.RL_ORDER_A_LAYOUT, "b_layout": L.RL_ORDER_B_LAYOUT,
+          "c_atb": L.RL_ORDER_C_ATB}
+A_FORMATS = {"bf16": L.RL_A_BF16, "bf16_quantize": L.RL_A_BF16_QUANTIZE, "packed_rowblock": L.RL_A_PACKED_ROWBLOCK,
+             "packed_a_layout": L.RL_A_PACKED_A_LAYOUT}
+ACTS = {None: L.RL_ACT_NONE, "none": L.RL_ACT_NONE, "gelu_tanh": L.RL_ACT_GELU_TANH, "swiglu": L.RL_ACT_SWIGLU}
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _dev(t, name):
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise TypeError(f"{name} must be a torch tensor on a ROCm device")
+    return t
+
+
+def packed_bytes(rows, cols):
+    """Bytes of a packed stream of rows x cols values."""
+    if cols % 8:
+        raise ValueError("cols must be a multiple of 8")
+    return rows * cols // 8 * 9
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# quantize / dequantize
+# ---------------------------------------------------------------------------------------------------------------
+
+def quantize(x, order="rowblock", packed=True, deq=False):
+    """Encode an (R, C) float32 or bf16 tensor to bfp16 blocks of 8 consecutive columns, bit-exact to
+    npu_layouts.to_bfp16 (redline/npu_layouts.py:62-73) applied to the layout `order`.
+
+    Returns (packed uint8 [R*C/8*9] or None, deq bf16 (R, C) or None); ``deq`` holds the decoded values, which
+    rl_bfp16_gemm consumes directly (a_fmt="bf16")."""
+    _dev(x, "x")
+    if x.dim() != 2 or x.dtype not in (torch.float32, torch.bfloat16) or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D float32/bfloat16 tensor with unit column stride")
+    R, C = x.shape
+    p = torch.empty(packed_bytes(R, C), dtype=torch.uint8, device=x.device) if packed else None
+    q = torch.empty((R, C), dtype=torch.bfloat16, device=x.device) if deq else None
+    dt = L.RL_DTYPE_BF16 if x.dtype == torch.bfloat16 else L.RL_DTYPE_F32
+    L.check(L.lib().rl_bfp16_quantize(_ptr(x), dt, R, C, x.stride(0), ORDERS[order], _ptr(p), _ptr(q), _stream(x)))
+    return p, q
+
+
+def dequantize(packed, rows, cols, order="rowblock", dtype=torch.float32):
+    """Decode a packed stream back to an (rows, cols) tensor (exact); for order "b_layout" the result is W (N, K)."""
+    _dev(packed, "packed")
+    out = torch.empty((rows, cols), dtype=dtype, device=packed.device)
+    dt = L.RL_DTYPE_BF16 if dtype == torch.bfloat16 else L.RL_DTYPE_F32
+    L.check(L.lib().rl_bfp16_dequantize(_ptr(packed), ORDERS[order], rows, cols, _ptr(out), dt, _stream(packed)))
+    return out
+
+
+def pack_weight(W):
+    """Linear weight W (N, K) on the device -> the packed B stream of B = W.T, byte-identical to
+    pack_weights.pack_b(W.T) (redline/pack_weights.py:72-79)."""
+    p, _ = quantize(W, order="b_layout")
+    return p
+
+
+def interleave_up(wg, wp):
+    """gate / proj weights (F, K) -> the Linear weight (2F, K) whose transpose is pack_weights.interleave_up's B:
+    rows [gate 64 | proj 64] per group of 128 (redline/pack_weights.py:82-89)."""
+    F, K = wg.shape
+    if wp.shape != (F, K) or F % 64:
+        raise ValueError("gate and proj must both be (F, K) with F % 64 == 0")
+    return torch.stack([wg.reshape(F // 64, 64, K), wp.reshape(F // 64, 64, K)], 1).reshape(2 * F, K)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# GEMM
+# ---------------------------------------------------------------------------------------------------------------
+
+def _epilogue(act, bias, gate, gate_split_row, residual, quantize_out):
+    ep = L.Epilogue()
+    ep.act = ACTS[act]
+    ep.flags = L.RL_EP_QUANTIZE_OUT if quantize_out else 0
+    for name, t, dt in (("bias", bias, torch.float32), ("gate", gate, torch.float32),
+                        ("residual", residual, torch.bfloat16)):
+        if t is not None:
+            _dev(t, name)
+            if t.dtype != dt or not t.is_contiguous() and name != "residual":
+                raise ValueError(f"{name} must be a contiguous {dt} tensor")
+    ep.bias = bias.data_ptr() if bias is not None else None
+    ep.gate = gate.data_ptr() if gate is not None else None
+    ep.gate_split_row = int(gate_split_row)
+    if residual is not None:
+        if residual.dim() != 2 or residual.stride(1) != 1:
+            raise ValueError("residual must be 2-D with unit column stride")
+        ep.residual = residual.data_ptr()
+        ep.ld_residual = residual.stride(0)
+    return ep
+
+
+def _check_ep_sizes(M, N, nout, bias, gate, gate_split_row, residual):
+    """Sizes the kernel reads from the epilogue vectors (the C ABI takes bare pointers)."""
+    if bias is not None and bias.numel() != N:
+        raise ValueError(f"bias must hold N = {N} values")
+    if gate is not None and gate.numel() != (2 * nout if gate_split_row > 0 else nout) \
+            and not (gate_split_row == 0 and gate.numel() == 2 * nout):
+        raise ValueError(f"gate must hold {nout} values ({2 * nout} with gate_split_row > 0)")
+    if residual is not None and (residual.shape[0] < M or residual.shape[1] < nout):
+        raise ValueError(f"residual must be at least ({M}, {nout})")
+
+
+def _a_args(a, a_fmt, M, K):
+    if a_fmt in ("bf16", "bf16_quantize"):
+        if a.dtype != torch.bfloat16 or a.dim() != 2 or a.stride(1) != 1 or a.shape[1] != K:
+            raise ValueError(f"A must be a (M, {K}) bfloat16 tensor with unit column stride")
+        return a.stride(0)
+    if a.dtype != torch.uint8 or a.numel() != packed_bytes(M, K):
+        raise ValueError(f"packed A must hold {packed_bytes(M, K)} bytes")
+    return K
+
+
+def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None, gate_split_row=0,
+         residual=None, quantize_out=False, out=None):
+    """C = epilogue(A @ B) with B the packed weight stream of a (K, N) matrix, bf16 output (M, N) (or (M, N/2) for
+    act="swiglu"). See rl_bfp16_gemm in include/rlbfp.h for the epilogue order."""
+    _dev(a, "A")
+    _dev(b_packed, "B")
+    if M is None:
+        if a_fmt not in ("bf16", "bf16_quantize"):
+            raise ValueError("M is required for packed A")
+        M = a.shape[0]
+    lda = _a_args(a, a_fmt, M, K)
+    if b_packed.dtype != torch.uint8 or b_packed.numel() != packed_bytes(K, N):
+        raise ValueError(f"B must be a uint8 stream of {packed_bytes(K, N)} bytes")
+    nout = N // 2 if act == "swiglu" else N
+    if out is None:
+        out = torch.empty((M, nout), dtype=torch.bfloat16, device=a.device)
+    elif out.dtype != torch.bfloat16 or out.shape != (M, nout) or out.stride(1) != 1:
+        raise ValueError(f"out must be ({M}, {nout}) bfloat16 with unit column stride")
+    _check_ep_sizes(M, N, nout, bias, gate, gate_split_row, residual)
+    ep = _epilogue(act, bias, gate, gate_split_row, residual, quantize_out)
+    L.check(L.lib().rl_bfp16_gemm(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M, N, K,
+                                  ctypes.byref(ep), _stream(a)))
+    return out
+
+
+class GemmSpec:
+    """One GEMM of a grouped launch (same arguments as gemm(); A is bf16 for every member)."""
+
+    def __init__(self, a, b_packed, N, K, act=None, bias=None, gate=None, gate_split_row=0, residual=None,
+                 quantize_out=False, out=None):
+        self.a, self.b, self.N, self.K = a, b_packed, N, K
+        self.ep_args = (act, bias, gate, gate_split_row, residual, quantize_out)
+        nout = N // 2 if act == "swiglu" else N
+        self.out = out if out is not None else torch.empty((a.shape[0], nout), dtype=torch.bfloat16,
+                                                           device=a.device)
+
+
+def gemm_grouped(specs, a_fmt="bf16"):
+    """Several independent GEMMs in one launch; returns their outputs."""
+    if not 1 <= len(specs) <= L.RL_MAX_GROUP:
+        raise ValueError(f"1..{L.RL_MAX_GROUP} GEMMs per group")
+    arr = (L.GemmDesc * len(specs))()
+    keep = []
+    for i, s in enumerate(specs):
+        _dev(s.a, "A")
+        M = s.a.shape[0]
+        arr[i].A = s.a.data_ptr()
+        arr[i].lda = _a_args(s.a, a_fmt, M, s.K)
+        arr[i].B_packed = s.b.data_ptr()
+        arr[i].C = s.out.data_ptr()
+        arr[i].ldc = s.out.stride(0)
+        arr[i].M, arr[i].N, arr[i].K = M, s.N, s.K
+        act, bias, gate, split, res, _q = s.ep_args
+        _check_ep_sizes(M, s.N, s.out.shape[1], bias, gate, split, res)
+        arr[i].ep = _epilogue(*s.ep_args)
+        keep.append(s)
+    L.check(L.lib().rl_bfp16_gemm_grouped(arr, len(specs), A_FORMATS[a_fmt], _stream(specs[0].a)))
+    return [s.out for s in specs]
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# GEMV
+# ---------------------------------------------------------------------------------------------------------------
+
+def gemv(x, b_packed, N, act="silu", out=None):
+    """y (M, N) bf16 = act(x) @ B for 1 <= M <= 8, x (M, K) bf16, act "silu" or None; fp32 accumulation."""
+    _dev(x, "x")
+    _dev(b_packed, "B")
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D bfloat16 tensor with unit column stride")
+    M, K = x.shape
+    if b_packed.dtype != torch.uint8 or b_packed.numel() != packed_bytes(K, N):
+        raise ValueError(f"B must be a uint8 stream of {packed_bytes(K, N)} bytes")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    code = L.RL_GEMV_SILU if act == "silu" else L.RL_ACT_NONE
+    L.check(L.lib().rl_bfp16_gemv(_ptr(x), x.stride(0), _ptr(b_packed), _ptr(out), out.stride(0), M, N, K, code,
+                                  _stream(x)))
+    return out

@@ -1,0 +1,100 @@
+"""The C ABI without a GPU: the library loads, exports every function include/rlbfp.h declares, and its host-side
+validators reject bad shapes with the documented codes."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from rlbfp import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "rlbfp.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    lib = L.lib()
+    names = header_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_version_and_sizes():
+    assert L.lib().rl_version().decode().startswith("rlbfp")
+    assert L.lib().rl_packed_bytes(4096, 3072) == 4096 * 3072 // 8 * 9
+    assert L.lib().rl_packed_bytes(1, 7) == -1
+
+
+@pytest.mark.parametrize("args,code", [
+    ((L.RL_DTYPE_BF16, 128, 64, 64, L.RL_ORDER_ROWBLOCK), L.RL_OK),
+    ((L.RL_DTYPE_BF16, 128, 60, 64, L.RL_ORDER_ROWBLOCK), L.RL_ERR_SHAPE),
+    ((L.RL_DTYPE_F32, 100, 64, 64, L.RL_ORDER_A_LAYOUT), L.RL_ERR_SHAPE),
+    ((L.RL_DTYPE_F32, 512, 1024, 1024, L.RL_ORDER_C_ATB), L.RL_OK),
+    ((L.RL_DTYPE_F32, 512, 512, 512, L.RL_ORDER_C_ATB), L.RL_ERR_SHAPE),
+    ((7, 128, 64, 64, L.RL_ORDER_ROWBLOCK), L.RL_ERR_ARG),
+    ((L.RL_DTYPE_F32, 128, 64, 32, L.RL_ORDER_ROWBLOCK), L.RL_ERR_SHAPE),
+    ((L.RL_DTYPE_F32, 128, 64, 64, 9), L.RL_ERR_ARG),
+])
+def test_validate_quantize(args, code):
+    assert L.lib().rl_validate_quantize(*args) == code
+    if code:
+        assert L.lib().rl_last_error().decode()
+
+
+def ep(act=0, flags=0, residual=None, ld=0, split=0):
+    e = L.Epilogue()
+    e.act, e.flags, e.residual, e.ld_residual, e.gate_split_row = act, flags, residual, ld, split
+    return ctypes.byref(e)
+
+
+@pytest.mark.parametrize("a_fmt,lda,ldc,M,N,K,e,code", [
+    (L.RL_A_BF16, 3072, 9216, 4352, 9216, 3072, None, L.RL_OK),
+    (L.RL_A_BF16, 3072, 12288, 4352, 24576, 3072, ep(L.RL_ACT_SWIGLU), L.RL_OK),
+    (L.RL_A_BF16, 3072, 12288, 4352, 24576, 3072, ep(L.RL_ACT_NONE), L.RL_ERR_ALIGN),  # ldc < N
+    (L.RL_A_BF16, 3072, 3072, 1, 3072, 3072, None, L.RL_OK),
+    (L.RL_A_BF16, 3072, 3072, 0, 3072, 3072, None, L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3072, 3072, 64, 3000, 3072, None, L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3072, 3072, 64, 3072, 3000, None, L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3071, 3072, 64, 3072, 3072, None, L.RL_ERR_ALIGN),
+    (L.RL_A_PACKED_A_LAYOUT, 0, 3072, 100, 3072, 3072, None, L.RL_ERR_SHAPE),
+    (L.RL_A_PACKED_ROWBLOCK, 0, 3072, 100, 3072, 3072, None, L.RL_OK),
+    (9, 3072, 3072, 64, 3072, 3072, None, L.RL_ERR_ARG),
+    (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(act=5), L.RL_ERR_ARG),
+    (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(flags=4), L.RL_ERR_ARG),
+    (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(residual=1, ld=100), L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(split=-1), L.RL_ERR_ARG),
+])
+def test_validate_gemm(a_fmt, lda, ldc, M, N, K, e, code):
+    assert L.lib().rl_validate_gemm(a_fmt, lda, ldc, M, N, K, e) == code
+
+
+@pytest.mark.parametrize("args,code", [
+    ((3072, 18432, 1, 18432, 3072, L.RL_GEMV_SILU), L.RL_OK),
+    ((3072, 18432, 9, 18432, 3072, L.RL_GEMV_SILU), L.RL_ERR_SHAPE),
+    ((3072, 18432, 1, 18400, 3072, L.RL_GEMV_SILU), L.RL_ERR_SHAPE),
+    ((3072, 18432, 1, 18432, 3072, L.RL_ACT_SWIGLU), L.RL_ERR_ARG),
+    ((3000, 18432, 1, 18432, 3072, L.RL_ACT_NONE), L.RL_ERR_SHAPE),
+])
+def test_validate_gemv(args, code):
+    assert L.lib().rl_validate_gemv(*args) == code
+
+
+def test_null_pointers_rejected_before_any_gpu_call():
+    """Argument errors are reported before the device is touched, so they work on a machine without a GPU."""
+    lib = L.lib()
+    s = lib.rl_bfp16_quantize(None, L.RL_DTYPE_BF16, 128, 64, 64, 0, None, None, None)
+    assert s == L.RL_ERR_NULL
+    s = lib.rl_bfp16_gemm(None, 0, 64, None, None, 128, 1, 128, 64, None, None)
+    assert s == L.RL_ERR_NULL
+    s = lib.rl_bfp16_gemv(None, 64, None, None, 128, 1, 128, 64, L.RL_GEMV_SILU, None)
+    assert s == L.RL_ERR_NULL
+    s = lib.rl_bfp16_gemm_grouped(None, 1, 0, None)
+    assert s == L.RL_ERR_NULL

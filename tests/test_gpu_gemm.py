@@ -1,0 +1,159 @@
+"""GPU GEMM against the CPU emulation (decoded operands, float64 matmul, epilogue, bf16): max |got - ref| /
+max |ref| <= 1e-2 (the reference's error metric, redline/run_glue.py:158-159), and element-wise within a bf16 ulp
+plus the fp32 summation difference."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bfp16 as F
+from oracle import gemm as G
+from rlbfp import ops
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def dev_t(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def setup(M, K, N, seed, outliers=0.0):
+    rng = np.random.default_rng(seed)
+    A = G.activations(rng, M, K, outliers=outliers)
+    W = G.linear_weight(rng, N, K)
+    packed = F.pack_b(W.T)
+    return rng, A, packed, F.quantize_rows(A), F.decode_b(packed, K, N)
+
+
+def check(got, ref, tol=TOL):
+    got = got.float().cpu().numpy()
+    assert got.shape == ref.shape
+    err = G.rel_err(got, ref)
+    assert err <= tol, f"rel err {err}"
+    # element-wise: within 2 bf16 ulps of the reference value, or tiny relative to the output scale
+    d = np.abs(got.astype(np.float64) - ref)
+    bound = 2 * np.abs(ref) * 2.0 ** -8 + 1e-4 * np.abs(ref).max()
+    assert (d <= bound).mean() > 0.999, f"{(d > bound).sum()} elements off"
+    return err
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 64, 256), (1, 64, 128), (100, 128, 384), (257, 192, 256),
+                                   (512, 512, 640), (4352, 256, 256)])
+def test_plain_shapes(dev, M, K, N):
+    rng, A, packed, Aq, Bq = setup(M, K, N, M + K + N)
+    a = dev_t(Aq, torch.bfloat16)
+    out = ops.gemm(a, dev_t(packed, torch.uint8), N, K)
+    check(out, G.gemm_ref(Aq, Bq))
+
+
+def test_output_canary_and_ldc(dev):
+    """Writes stay inside the (M, N) window of a wider output; rows past M are not written."""
+    M, K, N = 130, 128, 256
+    rng, A, packed, Aq, Bq = setup(M, K, N, 3)
+    big = torch.full((M + 5, N + 64), 7.0, dtype=torch.bfloat16, device="cuda")
+    ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, out=big[:M, :N])
+    check(big[:M, :N], G.gemm_ref(Aq, Bq))
+    assert (big[:, N:] == 7.0).all() and (big[M:, :] == 7.0).all()
+
+
+@pytest.mark.parametrize("a_fmt", ["bf16_quantize", "packed_rowblock", "packed_a_layout"])
+def test_a_formats_agree(dev, a_fmt):
+    """Every A format computes on the same bfp16 values: results identical to the bf16 (pre-quantized) path."""
+    M, K, N = 256, 192, 256
+    rng, A, packed, Aq, Bq = setup(M, K, N, 4, outliers=0.01)
+    b = dev_t(packed, torch.uint8)
+    ref = ops.gemm(dev_t(Aq, torch.bfloat16), b, N, K)
+    if a_fmt == "bf16_quantize":
+        a = dev_t(A, torch.bfloat16)
+    elif a_fmt == "packed_rowblock":
+        a = dev_t(F.to_bfp16(A.reshape(-1)), torch.uint8)
+    else:
+        a = dev_t(F.to_bfp16(F.a_layout(A)), torch.uint8)
+    got = ops.gemm(a, b, N, K, M=M, a_fmt=a_fmt)
+    assert torch.equal(got, ref)
+    check(got, G.gemm_ref(Aq, Bq))
+
+
+def test_bias_gelu(dev):
+    M, K, N = 200, 128, 384
+    rng, A, packed, Aq, Bq = setup(M, K, N, 5)
+    bias = (rng.standard_normal(N) * 0.5).astype(np.float32)
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, bias=dev_t(bias, torch.float32),
+                   act="gelu_tanh")
+    check(out, G.gemm_ref(Aq, Bq, bias=bias, act=G.ACT_GELU_TANH))
+
+
+def test_swiglu_interleaved(dev):
+    M, K, Fh = 300, 128, 256
+    rng = np.random.default_rng(6)
+    A = G.activations(rng, M, K)
+    wg, wp = G.linear_weight(rng, Fh, K), G.linear_weight(rng, Fh, K)
+    packed = F.pack_b(F.interleave_up(wg, wp))
+    Aq, Bq = F.quantize_rows(A), F.decode_b(packed, K, 2 * Fh)
+    bias = (rng.standard_normal(2 * Fh) * 0.1).astype(np.float32)
+    for kw in ({}, {"bias": bias}):
+        out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), 2 * Fh, K, act="swiglu",
+                       **{k: dev_t(v, torch.float32) for k, v in kw.items()})
+        assert out.shape == (M, Fh)
+        check(out, G.gemm_ref(Aq, Bq, act=G.ACT_SWIGLU, **kw))
+
+
+def test_gate_residual_split(dev):
+    M, K, N = 384, 256, 256
+    rng, A, packed, Aq, Bq = setup(M, K, N, 7)
+    res = F.bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    gate = rng.standard_normal((2, N)).astype(np.float32)
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, gate=dev_t(gate, torch.float32),
+                   gate_split_row=128, residual=dev_t(res, torch.bfloat16))
+    check(out, G.gemm_ref(Aq, Bq, gate=gate, gate_split_row=128, residual=res))
+
+
+def test_quantize_out(dev):
+    """Re-quantized output: every 8-column block is an exact bfp16 block (re-encoding it changes nothing except in
+    the -128 corner) and the values match the emulation."""
+    M, K, N = 256, 128, 256
+    rng, A, packed, Aq, Bq = setup(M, K, N, 8)
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, quantize_out=True).float()
+    o = out.cpu().numpy()
+    check(out, G.gemm_ref(Aq, Bq, quantize_out=True), tol=2e-2)
+    raw = F.to_bfp16(o.reshape(-1))
+    has_m128 = (raw.reshape(-1, 9)[:, 1:].view(np.int8) == -128).any(1)
+    same = (F.from_bfp16(raw).reshape(-1, 8) == o.reshape(-1, 8)).all(1)
+    assert same[~has_m128].all()
+
+
+def test_grouped_matches_single(dev):
+    rng = np.random.default_rng(9)
+    specs, refs = [], []
+    for M, K, N, act in ((4096 // 8, 128, 384, None), (256 // 4, 128, 256, "swiglu"), (130, 192, 128, None)):
+        A = G.activations(rng, M, K)
+        W = G.linear_weight(rng, N, K)
+        packed = F.pack_b(W.T)
+        Aq = F.quantize_rows(A)
+        a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)
+        specs.append(ops.GemmSpec(a, b, N, K, act=act))
+        refs.append(ops.gemm(a, b, N, K, act=act))
+    outs = ops.gemm_grouped(specs)
+    for o, r in zip(outs, refs):
+        assert torch.equal(o, r)
+
+
+def test_config1_full_size_rows(dev):
+    """BASELINE config 1 at full size (A 4096x3072 ~N(0,1), W 3072x3072 ~N(0,0.02), seed 0): the GPU quantize pass
+    feeds the GEMM; 256 sampled rows are checked against the emulation, and the quantized A bit-exact."""
+    rng = np.random.default_rng(0)
+    M = K = 4096
+    K, N = 3072, 3072
+    A = G.activations(rng, M, K)
+    W = G.linear_weight(rng, N, K)
+    a = dev_t(A, torch.bfloat16)
+    w = dev_t(W, torch.float32)
+    packed = ops.pack_weight(w)
+    p, aq = ops.quantize(a, deq=True)
+    out = ops.gemm(aq, packed, N, K)
+    rows = np.sort(rng.choice(M, 256, replace=False))
+    Aq = F.quantize_rows(A[rows])
+    np.testing.assert_array_equal(aq[torch.from_numpy(rows).cuda()].float().cpu().numpy(), Aq)
+    Bq = F.decode_b(packed.cpu().numpy(), K, N)
+    check(out[torch.from_numpy(rows).cuda()], G.gemm_ref(Aq, Bq))

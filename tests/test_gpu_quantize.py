@@ -1,0 +1,117 @@
+"""GPU encoder / decoder against the oracle: packed bytes bit-exact in every block order, decoded values exact."""
+
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bfp16 as F
+from oracle import bfp16_c as C
+from rlbfp import ops, layouts
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def to_dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def oracle_stream(x, order):
+    if order == "rowblock":
+        return F.to_bfp16(x.reshape(-1))
+    if order == "a_layout":
+        return F.to_bfp16(F.a_layout(x))
+    if order == "b_layout":
+        return F.pack_b(x.T)
+    return F.to_bfp16(F.c_layout_atb(x))
+
+
+def test_kat_vectors(dev):
+    with open(os.path.join(HERE, "golden", "bfp16_kat.json")) as f:
+        cases = json.load(f)["cases"]
+    x = np.array([[struct.unpack("<f", bytes.fromhex(h))[0] for h in c["x_f32_hex"]] for c in cases], np.float32)
+    p, q = ops.quantize(to_dev(x), deq=True)
+    got = p.cpu().numpy().reshape(-1, 9)
+    for i, c in enumerate(cases):
+        assert got[i].tobytes().hex() == c["bytes_hex"], c["why"]
+    want = np.array([np.array(c["q"], np.float64) * 2.0 ** (c["E"] - 133) for c in cases])
+    np.testing.assert_array_equal(q.float().cpu().numpy().astype(np.float64), want)
+
+
+@pytest.mark.parametrize("order,R,Cc", [("rowblock", 37, 72), ("rowblock", 4096, 3072), ("a_layout", 256, 192),
+                                        ("b_layout", 384, 256), ("c_atb", 512, 2048)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_orders_bit_exact(dev, order, R, Cc, dtype):
+    rng = np.random.default_rng(R * 7 + Cc)
+    x = (rng.standard_normal((R, Cc)) * np.exp(rng.uniform(-8, 8, (R, 1)))).astype(np.float32)
+    if dtype == torch.bfloat16:
+        x = F.bf16_round(x)
+    p, q = ops.quantize(to_dev(x, dtype), order=order, deq=True)
+    want = oracle_stream(x, order) if R * Cc < 2**22 else C.to_bfp16(x)
+    np.testing.assert_array_equal(p.cpu().numpy(), want)
+    np.testing.assert_array_equal(q.float().cpu().numpy(), F.quantize_rows(x))
+    back = ops.dequantize(p, R, Cc, order=order)
+    np.testing.assert_array_equal(back.cpu().numpy(), F.quantize_rows(x))
+
+
+def test_adversarial_blocks(dev):
+    """ties at every exponent, saturation, -128, zeros, float32 subnormals, signed zeros, infinities."""
+    rng = np.random.default_rng(11)
+    rows = []
+    for e in range(1, 250, 3):
+        step = 2.0 ** (e - 133)
+        rows.append((rng.integers(-127, 127, 8) + 0.5) * step)
+        rows.append(np.array([127.5, -127.5, 64.5, -64.5, 0.5, -0.5, 1.5, -2.5]) * step)
+    rows.append(rng.integers(-2**23 + 1, 2**23, 8) * 2.0 ** -149)      # subnormal block (E = 0)
+    rows.append(np.array([2**-149, -2**-149, 0, -0.0, 2**-140, 0, 0, 0]))
+    rows.append(np.array([np.inf, -np.inf, 1.0, 0, 0, 0, 0, 0]))        # E = 255, saturates
+    x = np.concatenate(rows).astype(np.float32).reshape(-1, 8)
+    p, q = ops.quantize(to_dev(x), deq=True)
+    np.testing.assert_array_equal(p.cpu().numpy(), C.to_bfp16(x))
+    np.testing.assert_array_equal(p.cpu().numpy(), F.to_bfp16(x))
+    fin = np.isfinite(x).all(1)
+    np.testing.assert_array_equal(q.float().cpu().numpy()[fin], F.quantize_rows(x)[fin])
+
+
+def test_truncate_variant_differs(dev):
+    x = np.array([[1.0, 2**-7, 3 * 2**-7, -2**-7, 255 / 128, -255 / 128, 5 * 2**-7, 0]], np.float32)
+    p, _ = ops.quantize(to_dev(x))
+    assert p.cpu().numpy().tobytes() == F.to_bfp16(x).tobytes()
+    assert p.cpu().numpy().tobytes() != F.to_bfp16(x, truncate=True).tobytes()
+
+
+def test_pack_weight_equals_pack_b(dev):
+    """The GPU packer writes the bytes of redline/pack_weights.py: to_bfp16(b_layout(W.T, 64, 128)), including the
+    SwiGLU interleave of the up weights."""
+    rng = np.random.default_rng(5)
+    K, Fh = 192, 128
+    wg = (rng.standard_normal((Fh, K)) * 0.02).astype(np.float32)
+    wp = (rng.standard_normal((Fh, K)) * 0.02).astype(np.float32)
+    W = ops.interleave_up(to_dev(wg), to_dev(wp))
+    got = ops.pack_weight(W.contiguous()).cpu().numpy()
+    np.testing.assert_array_equal(got, F.pack_b(F.interleave_up(wg, wp)))
+    np.testing.assert_array_equal(layouts.unpack_b(to_dev(got, torch.uint8), K, 2 * Fh).cpu().numpy(),
+                                  F.decode_b(got, K, 2 * Fh))
+
+
+def test_layout_names(dev):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal(8 * 1000).astype(np.float32)
+    raw = layouts.to_bfp16(to_dev(x))
+    np.testing.assert_array_equal(raw.cpu().numpy(), F.to_bfp16(x))
+    np.testing.assert_array_equal(layouts.from_bfp16(raw).cpu().numpy(), F.from_bfp16(F.to_bfp16(x)))
+
+
+def test_strided_input_and_small_stream(dev):
+    rng = np.random.default_rng(7)
+    big = rng.standard_normal((9, 48)).astype(np.float32)
+    x = to_dev(big)[:, :40]                      # ld 48, 40 columns
+    p, _ = ops.quantize(x)
+    np.testing.assert_array_equal(p.cpu().numpy(), F.to_bfp16(big[:, :40].reshape(-1)))
+    one = to_dev(big[:1, :8])                    # a single block: the decoder's window must not read past 9 bytes
+    p1, _ = ops.quantize(one)
+    np.testing.assert_array_equal(ops.dequantize(p1, 1, 8).cpu().numpy(), F.quantize_rows(big[:1, :8]))

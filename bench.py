@@ -148,7 +148,7 @@ def gpu_bench(steps, warmup):
     }
 
 
-def cpu_baseline(host, p_up, p_down, rows=1024):
+def cpu_baseline(host, p_up, p_down, rows=M, runs=3):
     """The oracle's numpy restatement of the reference CPU path on the first `rows` rows of the same workload:
     to_bfp16 of the activations, from_bfp16 of the activations and of the pre-packed weights (the same bytes the GPU
     uses; packing is an offline cost and is not timed), float32 BLAS matmul, SwiGLU, bf16 rounding, re-quantize,
@@ -160,15 +160,20 @@ def cpu_baseline(host, p_up, p_down, rows=1024):
     x, _wg, _wp, _wd, res, gate = host
     x = F.bf16_round(x[:rows])
     res = F.bf16_round(res[:rows])
-    t0 = time.perf_counter()
-    xq = F.quantize_rows(x)
-    acc = xq @ F.decode_b(p_up, K, 2 * FF)
-    gt = acc.reshape(rows, -1, 2, 64)
-    hv = gt[:, :, 0] / (1 + np.exp(-gt[:, :, 0])) * gt[:, :, 1]
-    hq = F.quantize_rows(F.bf16_round(hv.reshape(rows, FF).astype(np.float32)))
-    out = F.bf16_round((res + gate * (hq @ F.decode_b(p_down, FF, K))).astype(np.float32))
-    dt = time.perf_counter() - t0
-    assert out.shape == (rows, K)
+
+    def one():
+        t0 = time.perf_counter()
+        xq = F.quantize_rows(x)
+        acc = xq @ F.decode_b(p_up, K, 2 * FF)
+        gt = acc.reshape(rows, -1, 2, 64)
+        hv = gt[:, :, 0] / (1 + np.exp(-gt[:, :, 0])) * gt[:, :, 1]
+        hq = F.quantize_rows(F.bf16_round(hv.reshape(rows, FF).astype(np.float32)))
+        out = F.bf16_round((res + gate * (hq @ F.decode_b(p_down, FF, K))).astype(np.float32))
+        assert out.shape == (rows, K)
+        return time.perf_counter() - t0
+
+    one()                                        # warm-up
+    dt = sorted(one() for _ in range(runs))[runs // 2]
     flops = 2.0 * rows * K * 2 * FF + 2.0 * rows * FF * K
     threads = None
     try:
@@ -178,8 +183,9 @@ def cpu_baseline(host, p_up, p_down, rows=1024):
         pass
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s",
             "cores": threads or len(os.sched_getaffinity(0)), "kind": "port",
-            "sample": f"rows 0..{rows - 1} of the {M}-row FFN pair with the full weights decoded, {dt:.2f} s; numpy "
-                      f"float32 BLAS, {len(os.sched_getaffinity(0))} host cpus visible"}
+            "sample": f"the full FFN pair step ({rows} rows, weights decoded from the packed bytes each run), median "
+                      f"of {runs} runs after a warm-up, {dt:.2f} s per step; numpy float32 BLAS, "
+                      f"{len(os.sched_getaffinity(0))} host cpus visible"}
 
 
 def main():

@@ -150,7 +150,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep
       float v[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) v[k] = silu_f(gv[k]) * pv[k];
-      const int ocol = ((n0 + gc) >> 1) + 0;  // 64t + u with t = col / 128, u = col % 64 (gc % 128 < 64)
+      const int ocol = (((n0 + gc) >> 7) << 6) + ((n0 + gc) & 63);  // 64t + u, t = col / 128, u = col % 64
       const u32x4 o = finish_block(d, row, ocol, nout, v);
       *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
     }

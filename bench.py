@@ -132,14 +132,29 @@ def gpu_bench(steps, warmup):
     for i in range(12):
         ops.gemv(rng_x, copies[i % 6], GEMV_N, out=ym)
     torch.cuda.synchronize()
-    n_gemv = 240
+    # a ~10 us kernel launched from Python one call at a time measures the launch path, not the kernel: capture the
+    # rotation over the copies in a HIP graph and time its replays (no memset nodes; the GEMV writes every output)
+    per_graph = 60
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(per_graph):
+                ops.gemv(rng_x, copies[i % 6], GEMV_N, out=ym)
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    ref = ops.gemv(rng_x, copies[(per_graph - 1) % 6], GEMV_N)
+    assert torch.equal(ref, ym), "graph replay of the GEMV differs from the eager result"
+    reps = 4
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for i in range(n_gemv):
-        ops.gemv(rng_x, copies[i % 6], GEMV_N, out=ym)
+    for _ in range(reps):
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
-    us_gemv = e0.elapsed_time(e1) * 1e3 / n_gemv
+    us_gemv = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
     gemv_bytes = GEMV_K * GEMV_N * 9 / 8 + GEMV_K * 2 + GEMV_N * 2
     return {
         "host": host, "p_up": inp["up"].cpu().numpy(), "p_down": inp["down"].cpu().numpy(),

@@ -7,7 +7,7 @@
  * Conventions for every entry point:
  *   - pointers are device pointers (HIP global memory) unless stated; sizes are int64 element counts;
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); work is enqueued, never synchronised;
- *   - outputs are caller-allocated; no entry point allocates device memory (GEMV scratch is passed in);
+ *   - outputs are caller-allocated; no entry point allocates device memory;
  *   - the return value is RL_OK (0) or an RL_ERR_* code; rl_last_error() gives a message for the calling thread.
  * The reference's interfaces are Python (numpy host code and NPU artifacts run through XRT); each declaration cites
  * the reference function it replaces.
@@ -116,10 +116,11 @@ typedef struct rl_gemm_desc {
 int rl_bfp16_gemm_grouped(const rl_gemm_desc *descs, int32_t n, int32_t a_fmt, void *stream);
 
 /* ---- GEMV (adaLN modulation) -------------------------------------------------------------------------------------
- * y (M, N) bf16 = act(x) @ B, x (M, K) bf16 with leading dimension ldx, B packed in b_layout(64, 128) order,
- * 1 <= M <= 8, N % 16 == 0 (and N % 128 == 0 for the layout), K % 64 == 0; act = RL_ACT_NONE or RL_GEMV_SILU;
- * fp32 accumulation; x is not quantized. Replaces host_glue.modulation / linear(silu(te), W)
- * (redline/host_glue.py:22-28, :43-48), which the reference runs in numpy float32 on the host. */
+ * y (M, N) bf16 = Q(act(x)) @ B, x (M, K) bf16 with leading dimension ldx, B packed in b_layout(64, 128) order,
+ * 1 <= M <= 8, N % 128 == 0, K % 64 == 0; act = RL_ACT_NONE or RL_GEMV_SILU (evaluated in fp32); Q quantizes the
+ * activation to bfp16 blocks of 8 along K as the GEMM's A operand is, so every block product is exact in int32;
+ * fp32 accumulation, bf16 output. Replaces host_glue.modulation / linear(silu(te), W) (redline/host_glue.py:22-28,
+ * :43-48), which the reference runs in numpy float32 on the host. */
 enum { RL_GEMV_SILU = 3 };
 int rl_bfp16_gemv(const uint16_t *x, int64_t ldx, const uint8_t *B_packed, uint16_t *y, int64_t ldy, int64_t M,
                   int64_t N, int64_t K, int32_t act, void *stream);

@@ -16,8 +16,11 @@ matmul of the dequantized bfp16 operands):
          then rounded to bf16 (RNE), and optionally re-quantized to bfp16 along rows (quantize_out).
 
 The adaLN modulation GEMV (redline/host_glue.py:26-28,43-44: ``linear(silu(te), W)``) is emulated with the same
-decoded weights: y = bf16( act(x) @ B_q ) with act = silu or identity evaluated in float64 on the bf16 input; the
-activation is not quantized to bfp16 (it is 1 x K and costs nothing to keep exact).
+decoded weights: y = bf16( Q(act(x)) @ B_q ) with act = silu or identity evaluated on the bf16 input, rounded to
+float32 and quantized to bfp16 blocks of 8 along K (Q, the same encoder as the activations of the GEMM), i.e. both
+GEMV operands are bfp16 as in the reference's NPU GEMMs. The GPU evaluates silu in float32 with the hardware exp2 and
+reciprocal; where that moves a value across a bfp16 rounding boundary the results differ by one quantization step of
+one product, far inside the tolerance.
 """
 
 import numpy as np
@@ -83,13 +86,16 @@ def gemm_bf16_acts(A_bf16, packed_b, K, N, **ep):
 
 
 def gemv_ref(x, Bq, act="silu"):
-    """x (M, K) bf16 values as float32, decoded weights (K, N) -> bf16-rounded (M, N)."""
+    """x (M, K) bf16 values as float32, decoded weights (K, N) -> bf16-rounded (M, N): act(x) is evaluated in float64,
+    rounded to float32 and quantized to bfp16 blocks of 8 along K (the GEMM's activation encoding), then multiplied
+    with the decoded weights in float64."""
     v = np.asarray(x, dtype=np.float64)
     if act == "silu":
         v = silu(v)
     elif act != ACT_NONE:
         raise ValueError(act)
-    return F.bf16_round_f64(v @ np.asarray(Bq, dtype=np.float64))
+    a = F.quantize_rows(v.astype(np.float32))
+    return F.bf16_round_f64(a.astype(np.float64) @ np.asarray(Bq, dtype=np.float64))
 
 
 def rel_err(got, ref):

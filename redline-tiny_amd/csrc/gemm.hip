@@ -60,16 +60,39 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Scheduling pattern for one K step of the pipelined loop (two halves of 64 MFMAs, 16 A reads and ~104 decode
+// VALU ops each): four A reads up front, then per row fragment its 4 MFMAs with one A read (four fragments ahead)
+// and seven VALU ops between them, so that neither LDS latency nor the decode stalls the matrix pipe.
+__device__ __forceinline__ void interleave_schedule() {
+  constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
+#pragma unroll
+  for (int g = 0; g < 32; g++) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 1, 0);
+  }
+}
+
 // 16-byte chunk swizzle of the A tile: chunk c of row r is stored at chunk c ^ swz(r). A wave's ds_read_b128 of one
 // chunk column over 16 consecutive rows then spreads over all banks.
 __device__ __forceinline__ int a_swz(int r) { return (r >> 1) & 7; }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+// silu(x) = x * sigmoid(x) with the hardware exp2 and reciprocal (about 1e-6 relative; the epilogue rounds to bf16)
+__device__ __forceinline__ float silu_f(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
 __device__ __forceinline__ float gelu_tanh_f(float x) {
   // x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3)
   const float u2 = 1.5957691216057308f * (x + 0.044715f * x * x * x);
-  return x / (1.0f + __expf(-u2));
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * u2));
 }
 
 // float32 -> bf16 bits, round half to even (finite inputs).
@@ -78,27 +101,40 @@ __device__ __forceinline__ uint32_t bf16_rne(float v) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// max over the 8 lanes of each aligned 8-lane group (DPP: quad xor 1, quad xor 2, half-row mirror).
-__device__ __forceinline__ uint32_t max8(uint32_t x) {
-  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));
-  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));
-  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));
-  return x;
+// Re-quantize one block of 8 bf16 values (4 packed words) to bfp16, returned as bf16 words. The scaling is by
+// powers of two (v_ldexp) and the rounding is v_rndne (half to even), so the result equals the integer encoder's;
+// blocks whose exponent is below 7 (values and steps in the float32 subnormal range) take the integer path so that
+// the result does not depend on the denormal mode. -0 comes back as +0, as from_bfp16 gives it.
+__device__ __forceinline__ u32x4 requantize8(u32x4 o) {
+  const uint32_t w[4] = {o.x, o.y, o.z, o.w};
+  uint32_t E = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) E = max(E, max((w[k] >> 7) & 0xFFu, (w[k] >> 23) & 0xFFu));
+  if (E < 7u) return quantize_bf16x8(o);
+  uint32_t r[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    float v[2] = {__uint_as_float(w[k] << 16), __uint_as_float(w[k] & 0xFFFF0000u)};
+    uint32_t b[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const float q = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(v[t], 133 - (int)E)), 127.0f);
+      b[t] = __float_as_uint(__builtin_amdgcn_ldexpf(q, (int)E - 133) + 0.0f) >> 16;
+    }
+    r[k] = b[0] | (b[1] << 16);
+  }
+  return u32x4{r[0], r[1], r[2], r[3]};
 }
 
-// bf16 value (as bits) re-quantized to bfp16 with the block exponent shared by its 8-lane group, returned as bits.
-// Exact: the scaling is by powers of two and rint is half-to-even; -0 is returned as +0 like from_bfp16.
-__device__ __forceinline__ uint32_t requantize_bits(uint32_t b) {
-  const uint32_t E = max8((b >> 7) & 0xFFu);
-  const float v = __uint_as_float(b << 16);
-  float q = __builtin_rintf(__builtin_amdgcn_ldexpf(v, 133 - (int)E));
-  q = fminf(q, 127.0f);
-  const float d = __builtin_amdgcn_ldexpf(q, (int)E - 133) + 0.0f;
-  return __float_as_uint(d) >> 16;
-}
-
-constexpr int kEPitch = BN + 4;  // floats per row of the epilogue tile (the pad spreads 4 row groups over banks)
-static_assert(64 * kEPitch * 4 <= 3 * kAStage, "epilogue tile must fit the LDS allocation");
+// Epilogue tile in LDS for 64 rows x 256 columns of fp32 accumulators, "row-quad" layout: the 4 values of rows
+// 4q..4q+3 of column c are 16 contiguous bytes at float index (q * 256 + slot(c)) * 4, so a lane writes one MFMA
+// accumulator (4 rows, one column) with one 16-byte store and a reader of 8 consecutive columns of 4 rows issues
+// eight 16-byte loads. slot(c) = c ^ ((c >> 4) & 15) permutes columns inside their 16-column group, so that both the
+// writers (16 consecutive columns) and the readers (the same column offset of 16 neighbouring 8-column blocks) cover
+// all banks.
+constexpr int kEpFloats = 16 * 256 * 4;
+static_assert(kEpFloats * 4 <= 3 * kAStage, "epilogue tile must fit the LDS allocation");
+__device__ __forceinline__ int ep_slot(int c) { return c ^ ((c >> 4) & 15); }
 
 // 8 values of one output block: bias, activation, gate / residual, bf16 rounding (RNE) and the optional bfp16
 // re-quantize, all in fp32; returns the 8 bf16 as 4 words.
@@ -119,62 +155,69 @@ __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int oc
 #pragma unroll
   for (int k = 0; k < 8; k++) b[k] = bf16_rne(v[k]);
   u32x4 o = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
-  if (d.flags & RL_EP_QUANTIZE_OUT) o = quantize_bf16x8(o);
+  if (d.flags & RL_EP_QUANTIZE_OUT) o = requantize8(o);
   return o;
 }
 
 // Phase B of the epilogue for 64 rows starting at r0: the LDS tile holds the fp32 accumulators of computed columns
-// n0..n0+255 (row pitch kEPitch).
+// n0..n0+255 in the row-quad layout. Each thread takes 4 rows x 8 output columns (4 output blocks).
 __device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep, int r0, int n0, int nout, int tid) {
+  auto quad = [&](int q, int c) { return *reinterpret_cast<const f32x4*>(ep + (q * 256 + ep_slot(c)) * 4); };
   if (d.act == RL_ACT_SWIGLU) {
-    // 64 rows x 128 output columns = 1024 blocks; block b: row b / 16, output block b % 16 of this tile
+    // 16 row quads x 16 gate blocks of 8 columns: one per thread; gate columns gc..gc+7, proj gc+64..gc+71
+    const int q = tid >> 4, ob = tid & 15;
+    const int gc = (ob >> 3) * 128 + (ob & 7) * 8;
+    if (n0 + gc >= d.N) return;
+    f32x4 g[8], p[8];
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int b = it * kGThreads + tid;
-      const int rr = b >> 4, ob = b & 15;
-      const int gc = (ob >> 3) * 128 + (ob & 7) * 8;  // gate column in the tile; proj = gc + 64
-      const int row = r0 + rr;
-      if (row >= d.M || n0 + gc >= d.N) continue;
-      const float* src = ep + rr * kEPitch + gc;
-      const f32x4 g0 = *reinterpret_cast<const f32x4*>(src), g1 = *reinterpret_cast<const f32x4*>(src + 4);
-      const f32x4 p0 = *reinterpret_cast<const f32x4*>(src + 64), p1 = *reinterpret_cast<const f32x4*>(src + 68);
-      float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-      float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-      if (d.bias) {
+    for (int k = 0; k < 8; k++) {
+      g[k] = quad(q, gc + k);
+      p[k] = quad(q, gc + 64 + k);
+    }
+    float bg[8], bp[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-          gv[k] += d.bias[n0 + gc + k];
-          pv[k] += d.bias[n0 + gc + 64 + k];
-        }
-      }
+    for (int k = 0; k < 8; k++) {
+      bg[k] = d.bias ? d.bias[n0 + gc + k] : 0.f;
+      bp[k] = d.bias ? d.bias[n0 + gc + 64 + k] : 0.f;
+    }
+    const int ocol = (((n0 + gc) >> 7) << 6) + ((n0 + gc) & 63);  // 64t + u, t = col / 128, u = col % 64
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * q + i;
+      if (row >= d.M) break;
       float v[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = silu_f(gv[k]) * pv[k];
-      const int ocol = (((n0 + gc) >> 7) << 6) + ((n0 + gc) & 63);  // 64t + u, t = col / 128, u = col % 64
+      for (int k = 0; k < 8; k++) v[k] = silu_f(g[k][i] + bg[k]) * (p[k][i] + bp[k]);
       const u32x4 o = finish_block(d, row, ocol, nout, v);
       *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
     }
   } else {
-    // 64 rows x 256 columns = 2048 blocks; block b: row b / 32, column block b % 32
+    // 16 row quads x 32 column blocks: two per thread
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
+    for (int it = 0; it < 2; it++) {
       const int b = it * kGThreads + tid;
-      const int rr = b >> 5, cb = b & 31;
-      const int row = r0 + rr, col = n0 + cb * 8;
-      if (row >= d.M || col >= d.N) continue;
-      const float* src = ep + rr * kEPitch + cb * 8;
-      const f32x4 a0 = *reinterpret_cast<const f32x4*>(src), a1 = *reinterpret_cast<const f32x4*>(src + 4);
-      float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      if (d.bias) {
+      const int q = b >> 5, cb = b & 31;
+      const int col = n0 + cb * 8;
+      if (col >= d.N) continue;
+      f32x4 a[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] += d.bias[col + k];
-      }
-      if (d.act == RL_ACT_GELU_TANH) {
+      for (int k = 0; k < 8; k++) a[k] = quad(q, cb * 8 + k);
+      float bv[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = gelu_tanh_f(v[k]);
+      for (int k = 0; k < 8; k++) bv[k] = d.bias ? d.bias[col + k] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = r0 + 4 * q + i;
+        if (row >= d.M) break;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          v[k] = a[k][i] + bv[k];
+          if (d.act == RL_ACT_GELU_TANH) v[k] = gelu_tanh_f(v[k]);
+        }
+        const u32x4 o = finish_block(d, row, col, nout, v);
+        *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
       }
-      const u32x4 o = finish_block(d, row, col, nout, v);
-      *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
     }
   }
 }
@@ -280,9 +323,9 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
 
   bf16x8 bcur[4][2];
   // MFMAs of one K half (h) of one step over the 16 row fragments, with the A stage at st
-  // (A fragments are read three row fragments ahead of their MFMAs, so that LDS latency hides under MFMAs)
+  // (A fragments are read four row fragments ahead of their MFMAs, so that LDS latency hides under MFMAs)
   auto mfma_half = [&](const uint8_t* st, int aoff, int h) {
-    constexpr int kAhead = 3;
+    constexpr int kAhead = 4;
     bf16x8 a[kAhead];
 #pragma unroll
     for (int mf = 0; mf < kAhead; mf++) a[mf] = *reinterpret_cast<const bf16x8*>(st + mf * 16 * (BK * 2) + aoff);
@@ -301,34 +344,42 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
     // ---- pipelined path: A by direct-to-LDS loads into 3 stages, B windows in 3 register slots, both issued two
     // steps ahead. Within a step, the B half not being multiplied is decoded under the MFMAs of the other half:
     // first half (K 0..31 of the step) decodes this step's second half, second half decodes the next step's first.
-    uint32_t raw[3][4][2][3];
-    auto load_raw = [&](uint32_t (&r)[4][2][3], int kt) {
+    // Buffer loads: the per-lane byte offsets are fixed for the whole K loop and the K step enters as a scalar
+    // offset, so no per-step address registers are needed. Out-of-range offsets read zero.
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    const __amdgpu_buffer_rsrc_t brs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)d.B, (short)0, (int)((int64_t)d.K * d.N / 8 * 9), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)d.A, (short)0, (int)(((int64_t)d.M - 1) * d.lda * 2 + (int64_t)d.K * 2), 0x00020000);
+    uint32_t vb[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) vb[j] = (uint32_t)(bptr[j] - d.B);
+    u32x3 raw[3][4][2];
+    auto load_raw = [&](u32x3 (&r)[4][2], int kt) {
 #pragma unroll
       for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const uint32_t* p = reinterpret_cast<const uint32_t*>(bptr[j] + (int64_t)kt * kTileBytes + h * 576);
-          r[j][h][0] = p[0];
-          r[j][h][1] = p[1];
-          r[j][h][2] = p[2];
-        }
+        for (int h = 0; h < 2; h++) r[j][h] = __builtin_amdgcn_raw_buffer_load_b96(brs, vb[j] + h * 576, kt * kTileBytes, 0);
     };
-    auto decode_half = [&](const uint32_t (&r)[4][2][3], int h) {
+    auto decode_half = [&](const u32x3 (&r)[4][2], int h) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) bcur[j][h] = decode_window(r[j][h][0], r[j][h][1], r[j][h][2], bo);
+      for (int j = 0; j < 4; j++) bcur[j][h] = decode_window(r[j][h].x, r[j][h].y, r[j][h].z, bo);
     };
     // wave w fills rows 64w..64w+63 of a stage: 8 loads of 8 rows; lane l -> row +l/8, LDS chunk l%8, which holds
     // logical chunk (l%8) ^ swz(row)
-    const int dma_row = 64 * wave + (lane >> 3);
+    uint32_t va[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int r = 64 * wave + (lane >> 3) + 8 * i;
+      const int c = (lane & 7) ^ a_swz(r);
+      va[i] = (uint32_t)(((int64_t)min(m0 + r, d.M - 1) * d.lda + c * 8) * 2);
+    }
     auto dma_a = [&](int stage, int kt) {
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const int r = dma_row + 8 * i;
-        const int c = (lane & 7) ^ a_swz(r);
-        const int gr = min(m0 + r, d.M - 1);
-        const uint16_t* src = static_cast<const uint16_t*>(d.A) + (int64_t)gr * d.lda + kt * BK + c * 8;
         uint8_t* dst = lds + stage * kAStage + (64 * wave + 8 * i) * (BK * 2);
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16, va[i],
+                                                 kt * BK * 2, 0, 0);
       }
     };
 
@@ -351,10 +402,13 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
       }
       const uint8_t* st = lds + S * kAStage;
       if (active) {
+        // one basic block: decode of the other half (VALU) and A reads (LDS) interleaved with the MFMAs; the decode
+        // of the next step's first half runs even on the last step (its result is then unused)
         decode_half(raw[S], 1);
         mfma_half(st, aoff0, 0);
-        if (kt + 1 < KT) decode_half(raw[(S + 1) % 3], 0);
+        decode_half(raw[(S + 1) % 3], 0);
         mfma_half(st, aoff1, 1);
+        interleave_schedule();
       }
       // A(kt+1) must have landed before the barrier; the loads issued in this step may stay in flight
       if (more)
@@ -415,9 +469,9 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
   }
 
   // ---- epilogue: through LDS, 64 rows at a time ----------------------------------------------------------------
-  // Phase A: each wave writes its fp32 accumulators for 64 rows into a row-major LDS tile (pitch kEPitch floats).
-  // Phase B: each thread takes one 8-column output block of a row (one bfp16 block when re-quantizing), applies the
-  // epilogue in fp32 and writes 16 bytes of bf16; a wave writes 512 contiguous bytes per row.
+  // Phase A: each wave writes its fp32 accumulators for 64 rows into the row-quad LDS tile (one 16-byte store per
+  // accumulator). Phase B: each thread takes 4 rows x 8 output columns (each row's 8 columns are one bfp16 block when
+  // re-quantizing), applies the epilogue in fp32 and writes 16 bytes of bf16 per row.
   float* ep = reinterpret_cast<float*>(lds);
   const int col_in = lane & 15;
   const int row_in = 4 * (lane >> 4);
@@ -427,11 +481,10 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
     if (active) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int c = 16 * grp[j] + col_in;
+        const int c = ep_slot(16 * grp[j] + col_in);
 #pragma unroll
         for (int f = 0; f < 4; f++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) ep[(16 * f + row_in + i) * kEPitch + c] = acc[4 * P + f][j][i];
+          *reinterpret_cast<f32x4*>(ep + ((4 * f + (lane >> 4)) * 256 + c) * 4) = acc[4 * P + f][j];
       }
     }
     __syncthreads();
@@ -455,6 +508,8 @@ static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, 
   if (a_fmt >= RL_A_PACKED_ROWBLOCK && ((uintptr_t)A % 4)) return fail(RL_ERR_ALIGN, "packed A must be 4-byte aligned");
   if ((uintptr_t)B % 4) return fail(RL_ERR_ALIGN, "B must be 4-byte aligned");
   if ((uintptr_t)C % 16) return fail(RL_ERR_ALIGN, "C must be 16-byte aligned");
+  if (K * N / 8 * 9 > INT32_MAX || (M - 1) * lda * 2 + K * 2 > INT32_MAX || M * K / 8 * 9 > INT32_MAX)
+    return fail(RL_ERR_SHAPE, "an operand is above 2^31 bytes (buffer offsets are 32-bit)");
   if (ep && ep->residual && (((uintptr_t)ep->residual % 16) || ep->ld_residual % 8))
     return fail(RL_ERR_ALIGN, "residual must be 16-byte aligned with ld_residual %% 8 == 0");
   if (ep && ep->bias && ((uintptr_t)ep->bias % 4)) return fail(RL_ERR_ALIGN, "bias must be 4-byte aligned");

@@ -4,34 +4,70 @@
 // computes in numpy float32 on fp32 weights; here the weights are the packed b_layout(W.T, 64, 128) stream and the
 // work is one pass over it (K * N * 9/8 bytes), which is the HBM roofline.
 //
-// One wave per 16-column group of the b_layout: that group's 64 K x 16 columns are 1152 contiguous bytes in every
-// 64 x 128 tile, 128 blocks of 8 K. The wave walks 8 K tiles at a time: lane (c, br) = (l/8, l%8) reads the 144
-// contiguous, 16-byte aligned bytes of K tile 8b+c, K rows br*8..+7 (16 blocks, one per column), with nine
-// 16-byte loads, and accumulates 16 column sums per row of x. Each block costs eight sign-extending converts, 8 FMAs
-// per row of x and one scale FMA per row: sum_k x_k q_k * 2^(E-133). The 64 lanes' partial sums are then reduced
-// with a transposing butterfly so that lane 4j holds column j's total.
+// The packed stream is read once with coalesced 1 KB loads: a workgroup owns one 16-column group, which for every K
+// tile is 1152 contiguous bytes. Lanes re-read whole blocks (16 columns x 8 K) from LDS. The activation is quantized
+// to bfp16 blocks of 8 along K like the GEMM's A operand, so every block product is two int8 dot4 instructions and
+// one exact power-of-two scale. Lane sums are reduced with a transposing butterfly, the two waves' K halves in LDS.
 #include "rlbfp.h"
 #include "rlbfp_device.h"
 #include "rlbfp_host.h"
 
 namespace rl {
 
-constexpr int kVWaves = 4;
+constexpr int kVWaves = 2;                    // waves per workgroup; they split K
 constexpr int kVThreads = 64 * kVWaves;
+constexpr int kVIterBytes = 8 * 1152;         // one wave iteration: 8 K tiles of one 16-column group = 9 x 1 KB
 
-__device__ __forceinline__ float silu_v(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu_v(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
 
+// Workgroup = one 16-column group g of the b_layout (N tile g / 8, super-block g % 8), all of K. Wave w takes the
+// iterations it = w, w + 2, ... of 8 K tiles each. An iteration's 8 x 1152 bytes are read with 9 coalesced 1 KB
+// loads into registers, one iteration ahead; they pass through the wave's own 9 KB of LDS, from which lane
+// l = (run, br) = (l/8, l%8) reads its 16 blocks (K rows br*8..+7 of K tile 8 it + run, 16 columns) as 144 aligned
+// bytes at offset 144 l (a 36-dword stride, which covers all banks).
+//
+// act(x) of the lane's 8 K rows is quantized to one bfp16 block per row of x (E = largest float32 exponent field,
+// q = rint(v * 2^(133-E)) clipped to [-128, 127], as the activation encoder does), so that each weight block
+// contributes 2^(Ew + Ex - 266) * (qw . qx) with two 4-way int8 dot products, exactly in int32.
 template <int M, bool SILU>
-__global__ __launch_bounds__(kVThreads) void gemv_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                         const uint8_t* __restrict__ B, uint16_t* __restrict__ y,
-                                                         int64_t ldy, int32_t N, int32_t K) {
-  const int lane = threadIdx.x & 63;
-  const int g = blockIdx.x * kVWaves + (threadIdx.x >> 6);  // 16-column group
-  if (g * 16 >= N) return;
+__global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ B, uint16_t* __restrict__ y,
+    int64_t ldy, int32_t N, int32_t K) {
+  constexpr int S = 2;  // register slots: one iteration in flight while the other is used
+  __shared__ __attribute__((aligned(16))) uint8_t buf[kVWaves][kVIterBytes];
+  __shared__ float red[kVWaves][M][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int KT = K / 64;
-  const int nt = g >> 3, sbc = g & 7;
-  const int c = lane >> 3, br = lane & 7;
-  const uint8_t* base = B + ((int64_t)nt * KT) * 9216 + sbc * 1152 + br * 144;
+  const int iters = (KT + 7) / 8;
+  const int mine = wave < iters ? (iters - wave + kVWaves - 1) / kVWaves : 0;  // this wave's iterations
+  const int g = blockIdx.x, nt = g >> 3, sbc = g & 7;
+  const int run = lane >> 3, br = lane & 7;
+
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)B, (short)0, (int)((int64_t)K * N / 8 * 9), 0x00020000);
+  // load lane offsets: instruction i, lane l -> chunk ci = 64 i + l of the iteration, K tile ci / 72 of the 8, byte
+  // 16 (ci % 72) of that tile's 1152-byte run; the iteration's first K tile enters as the scalar offset. K tiles past
+  // the end read zeros (their offsets are beyond the stream or in the next column group) and are skipped below.
+  uint32_t voff[9];
+#pragma unroll
+  for (int i = 0; i < 9; i++) {
+    const int ci = 64 * i + lane;
+    voff[i] = (uint32_t)(((int64_t)nt * KT + ci / 72) * 9216 + sbc * 1152 + 16 * (ci % 72));
+  }
+  u32x4 w[S][9], xs[S][M];
+  auto gload = [&](int idx, u32x4 (&dw)[9], u32x4 (&dx)[M]) {
+    const int it = wave + kVWaves * idx;
+#pragma unroll
+    for (int i = 0; i < 9; i++)
+      dw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], it * 8 * 9216, 0));
+    const int kt = 8 * it + run;
+    if (kt < KT) {
+#pragma unroll
+      for (int m = 0; m < M; m++) dx[m] = *reinterpret_cast<const u32x4*>(x + m * ldx + kt * 64 + br * 8);
+    }
+  };
 
   float part[M][16];
 #pragma unroll
@@ -39,62 +75,72 @@ __global__ __launch_bounds__(kVThreads) void gemv_kernel(const uint16_t* __restr
 #pragma unroll
     for (int j = 0; j < 16; j++) part[m][j] = 0.f;
 
-  const int nbatch = (KT + 7) / 8;
-  u32x4 w[9];
-  auto load = [&](int b) {
-    const int kt = 8 * b + c;
-    if (kt < KT) {
-      const u32x4* p = reinterpret_cast<const u32x4*>(base + (int64_t)kt * 9216);
+  auto body = [&](int idx, const u32x4 (&dw)[9], const u32x4 (&xv)[M]) {
+    const int kt = 8 * (wave + kVWaves * idx) + run;
+    // realign through LDS: the coalesced chunks go in as loaded, each lane takes out its 144-byte run of blocks
 #pragma unroll
-      for (int i = 0; i < 9; i++) w[i] = __builtin_nontemporal_load(p + i);
-    }
-  };
-  load(0);
-  for (int b = 0; b < nbatch; b++) {
-    const int kt = 8 * b + c;
+    for (int i = 0; i < 9; i++) *reinterpret_cast<u32x4*>(&buf[wave][1024 * i + 16 * lane]) = dw[i];
     u32x4 cur[9];
 #pragma unroll
-    for (int i = 0; i < 9; i++) cur[i] = w[i];
-    if (b + 1 < nbatch) load(b + 1);
+    for (int i = 0; i < 9; i++) cur[i] = *reinterpret_cast<const u32x4*>(&buf[wave][144 * lane + 16 * i]);
     if (kt < KT) {
-      // activations of this lane's 8 K rows
-      float a[M][8];
+      uint32_t qx[M][2];
+      int ex[M];
 #pragma unroll
       for (int m = 0; m < M; m++) {
-        const u32x4 xv = *reinterpret_cast<const u32x4*>(x + m * ldx + kt * 64 + br * 8);
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+        const uint32_t xw[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
+        float v[8];
+        uint32_t e = 0;
 #pragma unroll
         for (int r = 0; r < 8; r++) {
-          const float v = __uint_as_float(r & 1 ? xw[r >> 1] & 0xFFFF0000u : xw[r >> 1] << 16);
-          a[m][r] = SILU ? silu_v(v) : v;
+          const float t = __uint_as_float(r & 1 ? xw[r >> 1] & 0xFFFF0000u : xw[r >> 1] << 16);
+          v[r] = SILU ? silu_v(t) : t;
+          e = max(e, (__float_as_uint(v[r]) >> 23) & 0xFFu);
         }
+        ex[m] = (int)e;
+        int qi[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+          qi[r] = (int)fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(v[r], 133 - (int)e)), 127.0f);
+        qx[m][0] = (qi[0] & 0xFF) | ((qi[1] & 0xFF) << 8) | ((qi[2] & 0xFF) << 16) | ((uint32_t)qi[3] << 24);
+        qx[m][1] = (qi[4] & 0xFF) | ((qi[5] & 0xFF) << 8) | ((qi[6] & 0xFF) << 16) | ((uint32_t)qi[7] << 24);
       }
       const uint32_t* wd = reinterpret_cast<const uint32_t*>(cur);
 #pragma unroll
       for (int j = 0; j < 16; j++) {
-        // block j: byte 9j = E, bytes 9j+1..9j+8 = q
-        const int e0 = 9 * j;
+        // block j (column j of the group, K rows br*8..+7): byte 9j = E, bytes 9j+1..9j+8 = q as two words
+        const int e0 = 9 * j, b1 = e0 + 1, b5 = e0 + 5;
         const uint32_t E = (wd[e0 >> 2] >> (8 * (e0 & 3))) & 0xFFu;
-        const float s = block_scale(E);
-        float q[8];
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-          const int bi = e0 + 1 + r;
-          q[r] = (float)(int8_t)(wd[bi >> 2] >> (8 * (bi & 3)));
-        }
+        const uint32_t lo = (b1 & 3) ? __builtin_amdgcn_alignbyte(wd[(b1 >> 2) + 1], wd[b1 >> 2], b1 & 3) : wd[b1 >> 2];
+        const uint32_t hi = (b5 & 3) ? __builtin_amdgcn_alignbyte(wd[(b5 >> 2) + 1], wd[b5 >> 2], b5 & 3) : wd[b5 >> 2];
 #pragma unroll
         for (int m = 0; m < M; m++) {
-          float dot = 0.f;
-#pragma unroll
-          for (int r = 0; r < 8; r++) dot = __builtin_fmaf(a[m][r], q[r], dot);
-          part[m][j] = __builtin_fmaf(dot, s, part[m][j]);
+          const int dot = __builtin_amdgcn_sdot4((int)lo, (int)qx[m][0],
+                                                 __builtin_amdgcn_sdot4((int)hi, (int)qx[m][1], 0, false), false);
+          part[m][j] += __builtin_amdgcn_ldexpf((float)dot, (int)E + ex[m] - 266);
         }
+      }
+    }
+  };
+
+  // ring of S register slots, loads S - 1 iterations ahead of the math
+#pragma unroll
+  for (int s0 = 0; s0 < S - 1; s0++)
+    if (s0 < mine) gload(s0, w[s0], xs[s0]);
+  for (int base = 0; base < mine; base += S) {
+#pragma unroll
+    for (int s0 = 0; s0 < S; s0++) {
+      const int idx = base + s0;
+      if (idx < mine) {
+        if (idx + S - 1 < mine) gload(idx + S - 1, w[(s0 + S - 1) % S], xs[(s0 + S - 1) % S]);
+        body(idx, w[s0], xs[s0]);
       }
     }
   }
 
-  // transposing butterfly: after the steps over lane bits 5..2, lane l holds the sum for column
-  // 8*b5 + 4*b4 + 2*b3 + b2 over the lanes that differ in those bits; bits 1..0 are then summed directly.
+  // reduce over the 64 lanes (run: lane bits 5..3, br: bits 2..0) with a transposing butterfly over bits 5..2
+  // (16 values -> 1; column 8 b5 + 4 b4 + 2 b3 + b2) and sums over bits 1 and 0; then over the two waves via LDS
+  const int col = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
 #pragma unroll
   for (int m = 0; m < M; m++) {
     float v[16];
@@ -102,27 +148,31 @@ __global__ __launch_bounds__(kVThreads) void gemv_kernel(const uint16_t* __restr
     for (int j = 0; j < 16; j++) v[j] = part[m][j];
     int cnt = 16;
 #pragma unroll
-    for (int s = 32; s >= 4; s >>= 1) {
-      const int half = cnt / 2;
-      const bool up = (lane & s) != 0;
+    for (int sb = 32; sb >= 4; sb >>= 1) {
+      const int hv = cnt / 2;
+      const bool up = (lane & sb) != 0;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        if (i < half) {
-          const float send = up ? v[i] : v[i + half];
-          const float keep = up ? v[i + half] : v[i];
-          v[i] = keep + __shfl_xor(send, s);
+        if (i < hv) {
+          const float send = up ? v[i] : v[i + hv];
+          const float keep = up ? v[i + hv] : v[i];
+          v[i] = keep + __shfl_xor(send, sb);
         }
       }
-      cnt = half;
+      cnt = hv;
     }
-    float t = v[0];
-    t += __shfl_xor(t, 2);
+    float t = v[0] + __shfl_xor(v[0], 2);
     t += __shfl_xor(t, 1);
-    if ((lane & 3) == 0) {
-      const int col = ((lane >> 5) & 1) * 8 + ((lane >> 4) & 1) * 4 + ((lane >> 3) & 1) * 2 + ((lane >> 2) & 1);
-      const uint32_t u = __float_as_uint(t);
-      y[m * ldy + g * 16 + col] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-    }
+    if ((lane & 3) == 0) red[wave][m][col] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < M * 16) {
+    const int m = threadIdx.x >> 4, c = threadIdx.x & 15;
+    float t = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kVWaves; w2++) t += red[w2][m][c];
+    const uint32_t u = __float_as_uint(t);
+    y[m * ldy + g * 16 + c] = (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
   }
 }
 
@@ -146,8 +196,9 @@ extern "C" int rl_bfp16_gemv(const uint16_t* x, int64_t ldx, const uint8_t* B_pa
   if (((uintptr_t)x % 16) || (ldx % 8)) return fail(RL_ERR_ALIGN, "x must be 16-byte aligned with ldx %% 8 == 0");
   if ((uintptr_t)B_packed % 16) return fail(RL_ERR_ALIGN, "B must be 16-byte aligned");
   if ((uintptr_t)y % 2) return fail(RL_ERR_ALIGN, "y must be 2-byte aligned");
+  if (K * N / 8 * 9 > INT32_MAX) return fail(RL_ERR_SHAPE, "packed B above 2^31 bytes");
   if ((s = check_device())) return s;
-  const dim3 grid((unsigned)(N / 16 / kVWaves));
+  const dim3 grid((unsigned)(N / 16));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool silu = act == RL_GEMV_SILU;
   switch (M) {

@@ -2,8 +2,8 @@
 
 The reference computes ``modulation(w, te) = linear(silu(te), W_mod)`` and ``norm_out_scale`` in numpy float32 on
 fp32 weights (redline/host_glue.py:22-28, :43-48), rows [t, 0]. Here W is the packed b_layout stream of W.T (packed
-once on the GPU with ``pack_linear``) and the product is the bandwidth-bound GEMV: y = bf16(silu(te) @ W.T) with fp32
-accumulation; te is bf16 and is not quantized.
+once on the GPU with ``pack_linear``) and the product is the bandwidth-bound GEMV: y = bf16(Q(silu(te)) @ W.T), with
+silu evaluated in fp32, Q the bfp16 activation encoding (blocks of 8 along K) and fp32 accumulation.
 """
 
 import torch

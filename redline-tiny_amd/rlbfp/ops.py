@@ -197,7 +197,8 @@ def gemm_grouped(specs, a_fmt="bf16"):
 # ---------------------------------------------------------------------------------------------------------------
 
 def gemv(x, b_packed, N, act="silu", out=None):
-    """y (M, N) bf16 = act(x) @ B for 1 <= M <= 8, x (M, K) bf16, act "silu" or None; fp32 accumulation."""
+    """y (M, N) bf16 = Q(act(x)) @ B for 1 <= M <= 8, x (M, K) bf16, act "silu" or None evaluated in fp32, Q the
+    bfp16 activation encoding (blocks of 8 along K); fp32 accumulation."""
     _dev(x, "x")
     _dev(b_packed, "B")
     if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:

@@ -76,5 +76,7 @@ def test_gemv_matches_loop():
     x = F.bf16_round(rng.standard_normal((2, K)).astype(np.float32))
     Bq = F.decode_b(F.pack_b(G.linear_weight(rng, N, K).T), K, N)
     got = G.gemv_ref(x, Bq)
-    want = F.bf16_round_f64(brute(G.silu(x), Bq))
+    a = F.quantize_rows(G.silu(x).astype(np.float32))     # the activation is quantized like the GEMM's A
+    want = F.bf16_round_f64(brute(a, Bq))
     np.testing.assert_array_equal(got, want)
+    assert not np.array_equal(got, F.bf16_round_f64(brute(G.silu(x), Bq)))   # and that quantization matters

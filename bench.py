@@ -203,13 +203,38 @@ def cpu_baseline(host, p_up, p_down, rows=M, runs=3):
                       f"{len(os.sched_getaffinity(0))} host cpus visible"}
 
 
+def copy_probe(mb, reps=10):
+    """D2D copies of `mb` MB: a kernel whose HBM bytes are known (mb MB read + mb MB written per launch)."""
+    import torch
+    n = mb * 2**20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    print(json.dumps({"copy_probe_mb": mb, "bytes_read": n, "bytes_written": n, "us": round(us, 2),
+                      "gbps_rw": round(2 * n / us / 1e3, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="only run device-to-device copies of MB megabytes (calibrates rocprofv3 FETCH_SIZE and "
+                         "WRITE_SIZE against a transfer of known size), print their bandwidth and exit")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by weight columns, "
               "see DESIGN.md, but multi-GPU runs are not part of this build)", file=sys.stderr)

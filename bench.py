@@ -27,6 +27,9 @@ for p in (ROOT, os.path.join(ROOT, "redline-tiny_amd")):
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (vendor figure)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+# HBM bytes per up-GEMM launch from rocprofv3 FETCH_SIZE (x2) and WRITE_SIZE (x1), the factors that make a 256 MB
+# device-to-device copy read and write 256 MB (profiles/gemm_dit_ffn_counters.md); re-measured when the kernel changes
+UP_GEMM_TRAFFIC_BYTES = 1_068_600_000
 M, K, FF = 4352, 3072, 12288
 GEMV_K, GEMV_N = 3072, 18432
 
@@ -255,7 +258,7 @@ def main():
                    "step": "quantize x + up GEMM (SwiGLU, re-quantized H) + down GEMM (gate*acc + residual)",
                    "weights": "bfp16ebs8 ~N(0,0.02)", "activations": "bf16 ~N(0,1)", "seed": 0},
         "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(up_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(up_tflops / PEAK_BF16_TFLOPS, 4), "traffic": UP_GEMM_TRAFFIC_BYTES,
                      "kernel": "gemm_kernel<bf16> up GEMM 4352x3072x24576 + SwiGLU", "us": round(r["ms_up"] * 1e3, 2)},
         "kernels": {
             "quantize_us": round(r["ms_q"] * 1e3, 2),

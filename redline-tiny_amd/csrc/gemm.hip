@@ -161,10 +161,12 @@ __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int oc
 
 // Phase B of the epilogue for 64 rows starting at r0: the LDS tile holds the fp32 accumulators of computed columns
 // n0..n0+255 in the row-quad layout. Each thread takes 4 rows x 8 output columns (4 output blocks).
+template <int NT>
 __device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep, int r0, int n0, int nout, int tid) {
   auto quad = [&](int q, int c) { return *reinterpret_cast<const f32x4*>(ep + (q * 256 + ep_slot(c)) * 4); };
   if (d.act == RL_ACT_SWIGLU) {
     // 16 row quads x 16 gate blocks of 8 columns: one per thread; gate columns gc..gc+7, proj gc+64..gc+71
+    if (tid >= 256) return;
     const int q = tid >> 4, ob = tid & 15;
     const int gc = (ob >> 3) * 128 + (ob & 7) * 8;
     if (n0 + gc >= d.N) return;
@@ -192,10 +194,10 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep
       *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
     }
   } else {
-    // 16 row quads x 32 column blocks: two per thread
+    // 16 row quads x 32 column blocks
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int b = it * kGThreads + tid;
+    for (int it = 0; it < 512 / NT; it++) {
+      const int b = it * NT + tid;
       const int q = b >> 5, cb = b & 31;
       const int col = n0 + cb * 8;
       if (col >= d.N) continue;
@@ -488,7 +490,207 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
       }
     }
     __syncthreads();
-    epilogue_rows(d, ep, m0 + 64 * P, n0, nout, tid);
+    epilogue_rows<kGThreads>(d, ep, m0 + 64 * P, n0, nout, tid);
+    __syncthreads();
+  };
+  pass.template operator()<0>();
+  pass.template operator()<1>();
+  pass.template operator()<2>();
+  pass.template operator()<3>();
+}
+
+// ---- 8-wave variant for bf16 A -------------------------------------------------------------------------------
+// Same 256 x 256 tile and K step, 8 waves (two per SIMD, so one wave's VALU work runs beside the other's MFMAs).
+// Wave (wm, wn) = (w / 4, w % 4) owns rows 128 wm .. +127 and the four 16-column groups of wn (SwiGLU: gate and proj
+// groups of one 128-column tile): 8 x 4 MFMA accumulators. B is decoded once per workgroup, four blocks per thread
+// per step, into a double-buffered bf16 LDS stage laid out in the b_layout block order, which is the MFMA operand
+// order (16 columns x 32 K = 1 KB, lane l = block l), so every operand read is a contiguous 1 KB.
+constexpr int kG8Threads = 512;
+constexpr int kBStage = 2 * 1024 * 16;  // decoded blocks of two 64 x 128 tiles, 16 bytes each
+static_assert(3 * kAStage + 2 * kBStage <= 160 * 1024, "LDS budget");
+
+__device__ __forceinline__ void interleave_schedule8() {
+  constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100, kDsWrite = 0x200;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, 6, 0);
+#pragma unroll
+  for (int g = 0; g < 16; g++) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kValu, 1, 0);
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> args) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kAStage + 2 * kBStage];
+  uint8_t* const bl = lds + 3 * kAStage;
+
+  const int pid = xcd_remap(blockIdx.x, gridDim.x);
+  int di = 0;
+  if constexpr (G > 1) {
+    for (int i = 1; i < args.n; i++)
+      if (pid >= args.d[i].tile_start) di = i;
+  }
+  const GemmDesc& d = args.d[di];
+  const int local = pid - d.tile_start;
+  const int group = local / (kGroupM * d.tiles_n);
+  const int first_m = group * kGroupM;
+  const int gm = min(d.tiles_m - first_m, kGroupM);
+  const int in_group = local - group * kGroupM * d.tiles_n;
+  const int m0 = (first_m + in_group % gm) * BM;
+  const int n0 = (in_group / gm) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int KT = d.K / BK;
+  const int N = d.N;
+
+  int grp[4];
+  if (d.act == RL_ACT_SWIGLU) {
+    const int g = 8 * (wn >> 1) + 2 * (wn & 1);
+    grp[0] = g; grp[1] = g + 1; grp[2] = g + 4; grp[3] = g + 5;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; j++) grp[j] = 4 * wn + j;
+  }
+  const bool active = n0 + 16 * grp[0] < d.N;
+
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)d.B, (short)0, (int)((int64_t)d.K * d.N / 8 * 9), 0x00020000);
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)d.A, (short)0, (int)(((int64_t)d.M - 1) * d.lda * 2 + (int64_t)d.K * 2), 0x00020000);
+
+  // decode assignment: thread t decodes blocks t + 512 r (r = 0..3) of the workgroup's two B tiles; windows of
+  // N tiles past N read zeros (offset beyond the stream) and their decode is never read
+  uint32_t vb[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int b = tid + 512 * r;
+    const int64_t ntile = (n0 >> 7) + (b >> 10);
+    const int64_t off = ntile < (d.N >> 7) ? (ntile * KT * kTileBytes + 9 * (b & 1023)) & ~(int64_t)3 : 0x7FFFFFF0;
+    vb[r] = (uint32_t)off;
+  }
+  const uint32_t bo = tid & 3;
+  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+  u32x3 raw[2][4];
+  auto load_raw = [&](u32x3 (&r)[4], int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) r[i] = __builtin_amdgcn_raw_buffer_load_b96(brs, vb[i], kt * kTileBytes, 0);
+  };
+  auto decode_store = [&](const u32x3 (&r)[4], uint8_t* stage) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      *reinterpret_cast<bf16x8*>(stage + 16 * (tid + 512 * i)) = decode_window(r[i].x, r[i].y, r[i].z, bo);
+  };
+  // A: wave w fills rows 32 w .. +31 of a stage, 4 loads of 8 rows
+  uint32_t va[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 32 * wave + (lane >> 3) + 8 * i;
+    const int c = (lane & 7) ^ a_swz(r);
+    va[i] = (uint32_t)(((int64_t)min(m0 + r, d.M - 1) * d.lda + c * 8) * 2);
+  }
+  auto dma_a = [&](int stage, int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      uint8_t* dst = lds + stage * kAStage + (32 * wave + 8 * i) * (BK * 2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16, va[i],
+                                               kt * BK * 2, 0, 0);
+    }
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int mf = 0; mf < 8; mf++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[mf][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int arow = lane & 15;
+  const int aoff[2] = {arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4),
+                       arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4)};
+  const int abase = 128 * wm * (BK * 2);
+
+  auto mfma_step = [&](const uint8_t* sa, const uint8_t* sb) {
+#pragma unroll
+    for (int kh = 0; kh < 2; kh++) {
+      bf16x8 b[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const bf16x8*>(sb + 2048 * grp[j] + 1024 * kh + 16 * lane);
+#pragma unroll
+      for (int mf = 0; mf < 8; mf++) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(sa + abase + mf * 16 * (BK * 2) + aoff[kh]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], acc[mf][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // prologue: A(0), A(1) in flight, B(0) decoded into stage 0, raw B(1) in flight
+  dma_a(0, 0);
+  load_raw(raw[0], 0);
+  if (KT > 1) {
+    dma_a(1, 1);
+    load_raw(raw[1], 1);
+  }
+  decode_store(raw[0], bl);
+  wait_vm<0>();
+  __syncthreads();
+
+  auto step = [&]<int R>(int kt) {
+    // R = kt % 2: raw slot R holds B(kt) (already decoded), slot R^1 holds B(kt+1)
+    const bool more = kt + 2 < KT;
+    if (more) {
+      dma_a((kt + 2) % 3, kt + 2);
+      load_raw(raw[R], kt + 2);
+    }
+    const uint8_t* sa = lds + (kt % 3) * kAStage;
+    const uint8_t* sb = bl + R * kBStage;
+    // B(kt+1) is decoded into the other stage under this step's MFMAs (on the last step the decode of stale
+    // registers lands in a stage that is never read again); inactive waves still decode their share
+    if (active) {
+      decode_store(raw[R ^ 1], bl + (R ^ 1) * kBStage);
+      mfma_step(sa, sb);
+      interleave_schedule8();
+    } else {
+      decode_store(raw[R ^ 1], bl + (R ^ 1) * kBStage);
+    }
+    if (more)
+      wait_vm<8>();  // this step's 4 A loads and 4 B windows may stay in flight
+    else
+      wait_vm<0>();
+    __syncthreads();
+  };
+  int kt = 0;
+  for (; kt + 2 <= KT; kt += 2) {
+    step.template operator()<0>(kt);
+    step.template operator()<1>(kt + 1);
+  }
+  if (kt < KT) step.template operator()<0>(kt);
+
+  // ---- epilogue (as the 4-wave kernel; pass P covers rows 64 P .. +63, held by the waves with wm = P / 2) --------
+  float* ep = reinterpret_cast<float*>(lds);
+  const int col_in = lane & 15;
+  const bool swiglu = d.act == RL_ACT_SWIGLU;
+  const int nout = swiglu ? N / 2 : N;
+  auto pass = [&]<int P>() {
+    if (active && wm == P / 2) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int c = ep_slot(16 * grp[j] + col_in);
+#pragma unroll
+        for (int f = 0; f < 4; f++)
+          *reinterpret_cast<f32x4*>(ep + ((4 * f + (lane >> 4)) * 256 + c) * 4) = acc[4 * (P % 2) + f][j];
+      }
+    }
+    __syncthreads();
+    epilogue_rows<kG8Threads>(d, ep, m0 + 64 * P, n0, nout, tid);
     __syncthreads();
   };
   pass.template operator()<0>();
@@ -535,7 +737,7 @@ static int launch(const GemmArgs<G>& args, int total_tiles, int32_t a_fmt, void*
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(total_tiles), block(kGThreads);
   switch (a_fmt) {
-    case RL_A_BF16: hipLaunchKernelGGL((gemm_kernel<RL_A_BF16, G>), grid, block, 0, st, args); break;
+    case RL_A_BF16: hipLaunchKernelGGL((gemm8_kernel<G>), grid, dim3(kG8Threads), 0, st, args); break;
     case RL_A_BF16_QUANTIZE: hipLaunchKernelGGL((gemm_kernel<RL_A_BF16_QUANTIZE, G>), grid, block, 0, st, args); break;
     case RL_A_PACKED_ROWBLOCK:
       hipLaunchKernelGGL((gemm_kernel<RL_A_PACKED_ROWBLOCK, G>), grid, block, 0, st, args);

@@ -132,6 +132,7 @@ __device__ __forceinline__ u32x4 requantize8(u32x4 o) {
 // eight 16-byte loads. slot(c) = c ^ ((c >> 4) & 15) permutes columns inside their 16-column group, so that both the
 // writers (16 consecutive columns) and the readers (the same column offset of 16 neighbouring 8-column blocks) cover
 // all banks.
+constexpr int kG8ThreadsDecl = 512;  // threads of the 8-wave kernel
 constexpr int kEpFloats = 16 * 256 * 4;
 static_assert(kEpFloats * 4 <= 3 * kAStage, "epilogue tile must fit the LDS allocation");
 __device__ __forceinline__ int ep_slot(int c) { return c ^ ((c >> 4) & 15); }
@@ -220,6 +221,34 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep
         const u32x4 o = finish_block(d, row, col, nout, v);
         *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
       }
+    }
+  }
+}
+
+// Second half of the 8-wave kernel's epilogue. The LDS tile holds fp32 values (bias, activation and the SwiGLU
+// product already applied) of `nquads` row quads x W staged columns in the row-quad layout; staged column c is output
+// column c0 + c. Each thread takes blocks of 4 rows x 8 columns: gate / residual, bf16 rounding, optional
+// re-quantize, one 16-byte store per row.
+template <int W>
+__device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, int r0, int c0, int nquads, int nout,
+                                          int tid) {
+  constexpr int kBlocks = W / 8;
+  for (int it = tid; it < nquads * kBlocks; it += kG8ThreadsDecl) {
+    const int q = it / kBlocks, cb = it % kBlocks;
+    const int col = c0 + 8 * cb;
+    if (col >= nout) continue;
+    f32x4 a[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * W + ep_slot(8 * cb + k)) * 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * q + i;
+      if (row >= d.M) break;
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = a[k][i];
+      const u32x4 o = finish_block(d, row, col, nout, v);
+      *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
     }
   }
 }
@@ -499,38 +528,55 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
   pass.template operator()<3>();
 }
 
-// ---- 8-wave variant for bf16 A -------------------------------------------------------------------------------
-// Same 256 x 256 tile and K step, 8 waves (two per SIMD, so one wave's VALU work runs beside the other's MFMAs).
-// Wave (wm, wn) = (w / 4, w % 4) owns rows 128 wm .. +127 and the four 16-column groups of wn (SwiGLU: gate and proj
-// groups of one 128-column tile): 8 x 4 MFMA accumulators. B is decoded once per workgroup, four blocks per thread
-// per step, into a double-buffered bf16 LDS stage laid out in the b_layout block order, which is the MFMA operand
-// order (16 columns x 32 K = 1 KB, lane l = block l), so every operand read is a contiguous 1 KB.
+// ---- 8-wave kernel for bf16 A ---------------------------------------------------------------------------------
+// Same 256 x 256 tile and K steps of 64, with 8 waves: one SIMD's MFMA pipe only stays full with two waves issuing.
+// Wave (wm, wn) = (w / 4, w % 4) owns rows 128 wm .. +127 and the four 16-column groups in B slots 4 wn .. 4 wn + 3:
+// 8 x 4 MFMA accumulators.
+//
+// LDS (160 KB): two A stages (256 x 64 bf16 with the 16-byte chunk swizzle, filled by direct-to-LDS buffer loads)
+// and three B stages. A B stage holds the 2048 decoded blocks of the tile's two b_layout tiles, 16 bytes each, in
+// MFMA operand order: slot s is one 16-column group x 64 K as two 1 KB fragments (K half h at 1024 h, lane l = block
+// l). Groups are put in slots at decode time so that each wave's four groups are adjacent (for SwiGLU, gate groups
+// {g, g+1} and proj groups {g+4, g+5} of one 128-column tile, so silu(gate) * proj pairs share lane and register).
+//
+// A K step is two phases, one per 32-deep half of K (32 MFMAs per wave). The operands of a phase are read into
+// registers during the phase before, so MFMAs never wait on LDS: A fragment mf of the next phase is read right after
+// the four MFMAs that consume A fragment mf of this phase (rotating registers); the next phase's B fragments are read
+// first. Per step k:
+//   phase 0: MFMAs on K half 0 of step k; read K half 1 of step k; load raw B(k+2) blocks r = 0, 1; decode raw
+//            B(k+1) blocks r = 2, 3 into B stage (k+1) % 3; wait for A(k+1); barrier (publishes A(k+1), B(k+1)).
+//   phase 1: MFMAs on K half 1 of step k; read K half 0 of step k+1; DMA A(k+2) into A stage k % 2 (its last reads
+//            were in phase 0, before the barrier); load raw B(k+2) blocks r = 2, 3; decode raw B(k+2) blocks r = 0, 1
+//            into B stage (k+2) % 3 (last read in phase 0 of step k-1).
+// The loop body has no branches, so the compiler's wait counts are exact; loads past the last step re-read step KT-1
+// and land in stages that are never read again.
 constexpr int kG8Threads = 512;
 constexpr int kBStage = 2 * 1024 * 16;  // decoded blocks of two 64 x 128 tiles, 16 bytes each
-static_assert(3 * kAStage + 2 * kBStage <= 160 * 1024, "LDS budget");
+static_assert(2 * kAStage + 3 * kBStage <= 160 * 1024, "LDS budget");
 
-__device__ __forceinline__ void interleave_schedule8() {
-  constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100, kDsWrite = 0x200;
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 6, 0);
+// Scheduling pattern for one quarter phase (8 MFMAs): the next phase's B fragment reads first (quarter 0), then the
+// quarter's buffer loads (at most two: a burst of them stalls instruction issue behind a full address queue), then
+// the MFMAs with kValu VALU ops after each and one A fragment read after every four; what remains (VALU, the LDS
+// store of a decoded block) goes last.
+template <int kB, int kLoads, int kValu>
+__device__ __forceinline__ void quarter_schedule() {
+  constexpr int kMfma = 0x008, kValuM = 0x002, kVmem = 0x060, kDsRead = 0x100, kDsWrite = 0x200;
+  if (kB) __builtin_amdgcn_sched_group_barrier(kDsRead, kB, 0);
+  if (kLoads) __builtin_amdgcn_sched_group_barrier(kVmem, kLoads, 0);
 #pragma unroll
-  for (int g = 0; g < 16; g++) {
+  for (int g = 0; g < 8; g++) {
     __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 1, 0);
+    if (kValu) __builtin_amdgcn_sched_group_barrier(kValuM, kValu, 0);
+    if (g % 4 == 3) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
   }
+  __builtin_amdgcn_sched_group_barrier(kValuM, 64, 0);
+  __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
 }
 
 template <int G>
 __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> args) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kAStage + 2 * kBStage];
-  uint8_t* const bl = lds + 3 * kAStage;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kAStage + 3 * kBStage];
+  uint8_t* const bl = lds + 2 * kAStage;
 
   const int pid = xcd_remap(blockIdx.x, gridDim.x);
   int di = 0;
@@ -551,14 +597,15 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   const int wm = wave >> 2, wn = wave & 3;
   const int KT = d.K / BK;
   const int N = d.N;
+  const bool swiglu = d.act == RL_ACT_SWIGLU;
 
+  // The 16-column groups of the tile in this wave's slots 4 wn + j: groups {g, g+1, g+4, g+5} of 128-column tile
+  // wn / 2, g = 2 (wn % 2) (for SwiGLU the gate and proj groups of the same output columns; the other activations
+  // use the same assignment)
   int grp[4];
-  if (d.act == RL_ACT_SWIGLU) {
+  {
     const int g = 8 * (wn >> 1) + 2 * (wn & 1);
     grp[0] = g; grp[1] = g + 1; grp[2] = g + 4; grp[3] = g + 5;
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; j++) grp[j] = 4 * wn + j;
   }
   const bool active = n0 + 16 * grp[0] < d.N;
 
@@ -567,45 +614,41 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       (void*)d.A, (short)0, (int)(((int64_t)d.M - 1) * d.lda * 2 + (int64_t)d.K * 2), 0x00020000);
 
-  // decode assignment: thread t decodes blocks t + 512 r (r = 0..3) of the workgroup's two B tiles; windows of
-  // N tiles past N read zeros (offset beyond the stream) and their decode is never read
-  uint32_t vb[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int b = tid + 512 * r;
-    const int64_t ntile = (n0 >> 7) + (b >> 10);
-    const int64_t off = ntile < (d.N >> 7) ? (ntile * KT * kTileBytes + 9 * (b & 1023)) & ~(int64_t)3 : 0x7FFFFFF0;
-    vb[r] = (uint32_t)off;
-  }
+  // B decode: thread t decodes blocks b = t + 512 r (r = 0..3) of the two tiles: tile h = r / 2, block bi = t +
+  // 512 (r % 2) in it, i.e. column group c = bi / 128, K half bi / 64 % 2, operand lane bi % 64. Its raw window
+  // starts at 9 bi rounded down to 4 bytes (offset t % 4 inside). The second tile's windows read zeros (offset past
+  // the stream, outside the range check) when it lies beyond N; its decode is never read.
+  const int64_t nt0 = n0 >> 7;
+  const uint32_t vb0 = (uint32_t)(nt0 * KT * kTileBytes + ((9 * tid) & ~3));
+  const uint32_t vb1 = nt0 + 1 < (N >> 7) ? (uint32_t)((nt0 + 1) * KT * kTileBytes + ((9 * tid) & ~3)) : 0x7FFFFFF0u;
   const uint32_t bo = tid & 3;
+  // LDS byte offset of block r inside a B stage: group G = 8 h + c goes to slot 4 (2 h + c / 2 % 2) + 2 (c / 4) +
+  // c % 2, so block r sits at st_off0 + (8 h + 2 (r % 2)) * 2048 (c = t / 128 + 4 (r % 2), h = r / 2)
+  const uint32_t st_off0 = (4 * ((tid >> 8) & 1) + ((tid >> 7) & 1)) * 2048 + ((tid >> 6) & 1) * 1024 + 16 * lane;
   typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-  u32x3 raw[2][4];
-  auto load_raw = [&](u32x3 (&r)[4], int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) r[i] = __builtin_amdgcn_raw_buffer_load_b96(brs, vb[i], kt * kTileBytes, 0);
+  u32x3 raw_a[2], raw_b[2];  // blocks r = 0, 1 and r = 2, 3
+  auto load_raw = [&](int r, int k) {
+    return __builtin_amdgcn_raw_buffer_load_b96(brs, r >= 2 ? vb1 : vb0, k * kTileBytes + (r & 1) * 9 * 512, 0);
   };
-  auto decode_store = [&](const u32x3 (&r)[4], uint8_t* stage) {
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      *reinterpret_cast<bf16x8*>(stage + 16 * (tid + 512 * i)) = decode_window(r[i].x, r[i].y, r[i].z, bo);
+  auto decode_store = [&](const u32x3& w, int r, uint8_t* stage) {
+    *reinterpret_cast<bf16x8*>(stage + st_off0 + (8 * (r >> 1) + 2 * (r & 1)) * 2048) = decode_window(w.x, w.y, w.z, bo);
   };
-  // A: wave w fills rows 32 w .. +31 of a stage, 4 loads of 8 rows
-  uint32_t va[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int r = 32 * wave + (lane >> 3) + 8 * i;
-    const int c = (lane & 7) ^ a_swz(r);
-    va[i] = (uint32_t)(((int64_t)min(m0 + r, d.M - 1) * d.lda + c * 8) * 2);
-  }
-  auto dma_a = [&](int stage, int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      uint8_t* dst = lds + stage * kAStage + (32 * wave + 8 * i) * (BK * 2);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16, va[i],
-                                               kt * BK * 2, 0, 0);
-    }
+  // A: wave w fills rows 32 w .. +31 of a stage, 4 loads of 8 rows: load i covers row r = 32 w + lane / 8 + 8 i,
+  // 16-byte chunk (lane % 8) ^ swz(r). swz(r + 8) = swz(r) ^ 4, so loads 0, 2 and loads 1, 3 differ by 16 rows
+  // only: two offset registers, recomputed at each use (the empty asm hides their values from the compiler, which
+  // would otherwise keep four loop-invariant registers). Rows past M lie past the end of the buffer resource and
+  // read zeros.
+  const int ar0 = 32 * wave + (lane >> 3);
+  const uint32_t va_e = (uint32_t)(((int64_t)(m0 + ar0) * d.lda + ((lane & 7) ^ a_swz(ar0)) * 8) * 2);
+  const uint32_t va_o = (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + ((lane & 7) ^ a_swz(ar0 + 8)) * 8) * 2);
+  const uint32_t va_16 = (uint32_t)(16 * d.lda * 2);
+  auto dma_a = [&](int stage, int k, int i) {
+    uint32_t v = (i & 1) ? va_o : va_e;
+    asm volatile("" : "+v"(v));
+    uint8_t* dst = lds + stage * kAStage + (32 * wave + 8 * i) * (BK * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16,
+                                             v + (i >> 1) * va_16, k * BK * 2, 0, 0);
   };
-
   f32x4 acc[8][4];
 #pragma unroll
   for (int mf = 0; mf < 8; mf++)
@@ -613,90 +656,153 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
     for (int j = 0; j < 4; j++) acc[mf][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int arow = lane & 15;
-  const int aoff[2] = {arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4),
-                       arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4)};
-  const int abase = 128 * wm * (BK * 2);
+  const uint32_t aoff0 = 128 * wm * (BK * 2) + arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
+  const uint32_t aoff1 = 128 * wm * (BK * 2) + arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
+  const uint32_t boff = 4 * wn * 2048 + 16 * lane;
 
-  auto mfma_step = [&](const uint8_t* sa, const uint8_t* sb) {
+  bf16x8 fa[8], fb0[4], fb1[4];
+  auto read_a = [&](const uint8_t* p, int mf) { return *reinterpret_cast<const bf16x8*>(p + mf * 16 * (BK * 2)); };
+  auto read_b = [&](const uint8_t* p, int j) { return *reinterpret_cast<const bf16x8*>(p + j * 2048); };
+
+  // prologue: B(0) decoded into stage 0 and A(0) landed; B(1) blocks 0, 1 decoded into stage 1, raw B(1) blocks 2, 3
+  // and A(1) in flight; K half 0 of step 0 read into registers
+  const int k1 = min(1, KT - 1);
 #pragma unroll
-    for (int kh = 0; kh < 2; kh++) {
-      bf16x8 b[4];
+  for (int i = 0; i < 4; i++) dma_a(0, 0, i);
+  raw_a[0] = load_raw(0, 0); raw_a[1] = load_raw(1, 0);
+  raw_b[0] = load_raw(2, 0); raw_b[1] = load_raw(3, 0);
+  wait_vm<0>();
+  decode_store(raw_a[0], 0, bl); decode_store(raw_a[1], 1, bl);
+  decode_store(raw_b[0], 2, bl); decode_store(raw_b[1], 3, bl);
+  raw_a[0] = load_raw(0, k1); raw_a[1] = load_raw(1, k1);
+  wait_vm<0>();
+  decode_store(raw_a[0], 0, bl + kBStage); decode_store(raw_a[1], 1, bl + kBStage);
+  // the loads in flight now are those of a phase 1, in its order, so the loop's wait counts hold on entry too
+  raw_b[0] = load_raw(2, k1); raw_b[1] = load_raw(3, k1);
 #pragma unroll
-      for (int j = 0; j < 4; j++) b[j] = *reinterpret_cast<const bf16x8*>(sb + 2048 * grp[j] + 1024 * kh + 16 * lane);
+  for (int i = 0; i < 4; i++) dma_a(1, k1, i);
+  __syncthreads();
 #pragma unroll
-      for (int mf = 0; mf < 8; mf++) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(sa + abase + mf * 16 * (BK * 2) + aoff[kh]);
+  for (int j = 0; j < 4; j++) fb0[j] = read_b(bl + boff, j);
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], acc[mf][j], 0, 0, 0);
+  for (int mf = 0; mf < 8; mf++) fa[mf] = read_a(lds + aoff0, mf);
+
+  // One phase of step k in four quarters of 8 MFMAs (scheduling fences between them). P = 0: MFMAs on K half 0 with
+  // fb0, reads K half 1 of step k into fa / fb1, loads raw B(kl) blocks 0, 1 (quarters 0, 1), decodes raw B(k+1)
+  // blocks 2, 3 into stage ds (quarters 0, 2). P = 1: MFMAs on K half 1 with fb1, reads K half 0 of step k+1 into
+  // fa / fb0, loads raw B(kl) blocks 2, 3 (quarter 0) and DMAs A(kl) into A stage sa (quarters 1, 2), decodes raw
+  // B(k+2) blocks 0, 1 into stage ds (quarters 0, 2).
+  auto quarter = [&]<int P, int Q>(bf16x8(&cur)[4], bf16x8(&nxt)[4], const uint8_t* na, const uint8_t* nb,
+                                   uint8_t* ds, int kl, int sa) {
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (Q == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) nxt[j] = read_b(nb, j);
+    }
+    if constexpr (P == 0) {
+      if constexpr (Q < 2) raw_a[Q] = load_raw(Q, kl);
+    } else {
+      if constexpr (Q == 0) {
+        raw_b[0] = load_raw(2, kl);
+        raw_b[1] = load_raw(3, kl);
+      } else if constexpr (Q < 3) {
+        dma_a(sa, kl, 2 * (Q - 1));
+        dma_a(sa, kl, 2 * (Q - 1) + 1);
       }
     }
+#pragma unroll
+    for (int mf = 2 * Q; mf < 2 * Q + 2; mf++) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mf], cur[j], acc[mf][j], 0, 0, 0);
+      fa[mf] = read_a(na, mf);
+    }
+    if constexpr (Q == 0 || Q == 2) {
+      if constexpr (P == 0)
+        decode_store(raw_b[Q / 2], 2 + Q / 2, ds);
+      else
+        decode_store(raw_a[Q / 2], Q / 2, ds);
+    }
+    constexpr int kL = P == 0 ? (Q < 2 ? 1 : 0) : (Q < 3 ? 2 : 0);
+    quarter_schedule<Q == 0 ? 4 : 0, kL, (Q == 0 || Q == 2) ? 3 : 0>();
+  };
+  auto phase = [&]<int P>(bf16x8(&cur)[4], bf16x8(&nxt)[4], const uint8_t* na, const uint8_t* nb, uint8_t* ds, int kl,
+                          int sa) {
+    quarter.template operator()<P, 0>(cur, nxt, na, nb, ds, kl, sa);
+    quarter.template operator()<P, 1>(cur, nxt, na, nb, ds, kl, sa);
+    quarter.template operator()<P, 2>(cur, nxt, na, nb, ds, kl, sa);
+    quarter.template operator()<P, 3>(cur, nxt, na, nb, ds, kl, sa);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // prologue: A(0), A(1) in flight, B(0) decoded into stage 0, raw B(1) in flight
-  dma_a(0, 0);
-  load_raw(raw[0], 0);
-  if (KT > 1) {
-    dma_a(1, 1);
-    load_raw(raw[1], 1);
+  int sb0 = 0, sb1 = 1, sb2 = 2;  // B stages of steps k, k+1, k+2
+  for (int k = 0; k < KT; k++) {
+    const int sa0 = k & 1;
+    const int kl = min(k + 2, KT - 1);
+    phase.template operator()<0>(fb0, fb1, lds + sa0 * kAStage + aoff1, bl + sb0 * kBStage + 1024 + boff,
+                                 bl + sb1 * kBStage, kl, sa0);
+    wait_vm<2>();  // A(k+1) done; raw B(k+2) blocks 0, 1 may stay in flight
+    __syncthreads();
+    phase.template operator()<1>(fb1, fb0, lds + (sa0 ^ 1) * kAStage + aoff0, bl + sb1 * kBStage + boff,
+                                 bl + sb2 * kBStage, kl, sa0);
+    const int t = sb0;
+    sb0 = sb1; sb1 = sb2; sb2 = t;
   }
-  decode_store(raw[0], bl);
   wait_vm<0>();
   __syncthreads();
 
-  auto step = [&]<int R>(int kt) {
-    // R = kt % 2: raw slot R holds B(kt) (already decoded), slot R^1 holds B(kt+1)
-    const bool more = kt + 2 < KT;
-    if (more) {
-      dma_a((kt + 2) % 3, kt + 2);
-      load_raw(raw[R], kt + 2);
-    }
-    const uint8_t* sa = lds + (kt % 3) * kAStage;
-    const uint8_t* sb = bl + R * kBStage;
-    // B(kt+1) is decoded into the other stage under this step's MFMAs (on the last step the decode of stale
-    // registers lands in a stage that is never read again); inactive waves still decode their share
-    if (active) {
-      decode_store(raw[R ^ 1], bl + (R ^ 1) * kBStage);
-      mfma_step(sa, sb);
-      interleave_schedule8();
-    } else {
-      decode_store(raw[R ^ 1], bl + (R ^ 1) * kBStage);
-    }
-    if (more)
-      wait_vm<8>();  // this step's 4 A loads and 4 B windows may stay in flight
-    else
-      wait_vm<0>();
-    __syncthreads();
-  };
-  int kt = 0;
-  for (; kt + 2 <= KT; kt += 2) {
-    step.template operator()<0>(kt);
-    step.template operator()<1>(kt + 1);
-  }
-  if (kt < KT) step.template operator()<0>(kt);
-
-  // ---- epilogue (as the 4-wave kernel; pass P covers rows 64 P .. +63, held by the waves with wm = P / 2) --------
+  // ---- epilogue --------------------------------------------------------------------------------------------
+  // Bias and activation (and for SwiGLU the product silu(gate) * proj, whose operands share lane and register) are
+  // applied in registers by all waves; the fp32 results are staged in LDS (row-quad layout, 128 KB) and finished
+  // 8 columns at a time by all threads. SwiGLU stages the whole tile (256 rows x 128 output columns) at once, the
+  // other activations 128 rows x 256 columns per pass.
   float* ep = reinterpret_cast<float*>(lds);
   const int col_in = lane & 15;
-  const bool swiglu = d.act == RL_ACT_SWIGLU;
   const int nout = swiglu ? N / 2 : N;
-  auto pass = [&]<int P>() {
-    if (active && wm == P / 2) {
+  float bj[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int c = ep_slot(16 * grp[j] + col_in);
+  for (int j = 0; j < 4; j++) bj[j] = (active && d.bias) ? d.bias[n0 + 16 * grp[j] + col_in] : 0.f;
+  if (swiglu) {
+    if (active) {
 #pragma unroll
-        for (int f = 0; f < 4; f++)
-          *reinterpret_cast<f32x4*>(ep + ((4 * f + (lane >> 4)) * 256 + c) * 4) = acc[4 * (P % 2) + f][j];
+      for (int jj = 0; jj < 2; jj++) {
+        const int tc = 16 * grp[jj] + col_in;
+        const int c = ep_slot(64 * (tc >> 7) + (tc & 63));
+#pragma unroll
+        for (int mf = 0; mf < 8; mf++) {
+          f32x4 v;
+#pragma unroll
+          for (int i = 0; i < 4; i++) v[i] = silu_f(acc[mf][jj][i] + bj[jj]) * (acc[mf][jj + 2][i] + bj[jj + 2]);
+          *reinterpret_cast<f32x4*>(ep + ((32 * wm + 4 * mf + (lane >> 4)) * 128 + c) * 4) = v;
+        }
       }
     }
     __syncthreads();
-    epilogue_rows<kG8Threads>(d, ep, m0 + 64 * P, n0, nout, tid);
-    __syncthreads();
-  };
-  pass.template operator()<0>();
-  pass.template operator()<1>();
-  pass.template operator()<2>();
-  pass.template operator()<3>();
+    ep8_finish<128>(d, ep, m0, n0 / 2, 64, nout, tid);
+  } else {
+    const bool gelu = d.act == RL_ACT_GELU_TANH;
+#pragma unroll
+    for (int P = 0; P < 2; P++) {
+      if (active && wm == P) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int c = ep_slot(16 * grp[j] + col_in);
+#pragma unroll
+          for (int mf = 0; mf < 8; mf++) {
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              v[i] = acc[mf][j][i] + bj[j];
+              if (gelu) v[i] = gelu_tanh_f(v[i]);
+            }
+            *reinterpret_cast<f32x4*>(ep + ((4 * mf + (lane >> 4)) * 256 + c) * 4) = v;
+          }
+        }
+      }
+      __syncthreads();
+      ep8_finish<256>(d, ep, m0 + 128 * P, n0, 32, nout, tid);
+      __syncthreads();
+    }
+  }
 }
 
 template <int G>

@@ -22,8 +22,10 @@ int ok() {
   return RL_OK;
 }
 
+static constexpr int kMaxDev = 64;
+static int g_cus[kMaxDev] = {0};
+
 int check_device() {
-  constexpr int kMaxDev = 64;
   static int state[kMaxDev] = {0};  // 0 unknown, 1 gfx950, 2 other
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -33,9 +35,18 @@ int check_device() {
   e = hipGetDeviceProperties(&prop, dev);
   if (e != hipSuccess) return fail(RL_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
   const bool is950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-  if (dev >= 0 && dev < kMaxDev) state[dev] = is950 ? 1 : 2;
+  if (dev >= 0 && dev < kMaxDev) {
+    g_cus[dev] = prop.multiProcessorCount;
+    state[dev] = is950 ? 1 : 2;
+  }
   if (!is950) return fail(RL_ERR_DEVICE, "device %d is %s; this library is built for gfx950 only", dev, prop.gcnArchName);
   return RL_OK;
+}
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev || g_cus[dev] <= 0) return 256;
+  return g_cus[dev];
 }
 
 int launch_status(const char* what) {

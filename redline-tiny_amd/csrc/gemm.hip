@@ -17,6 +17,7 @@
 //   * loads run two K steps ahead: while the MFMAs of step k run, the raw B windows and the A chunks of step k+1
 //     are in flight; after them B(k+1) is decoded and A(k+1) stored to the other LDS stage.
 //   * workgroups are remapped so each XCD walks a contiguous range of tiles, grouped 8 M-tiles at a time.
+#include <math.h>
 #include <stdio.h>
 
 #include "rlbfp.h"
@@ -554,17 +555,17 @@ constexpr int kG8Threads = 512;
 constexpr int kBStage = 2 * 1024 * 16;  // decoded blocks of two 64 x 128 tiles, 16 bytes each
 static_assert(2 * kAStage + 3 * kBStage <= 160 * 1024, "LDS budget");
 
-// Scheduling pattern for one quarter phase (8 MFMAs): the next phase's B fragment reads first (quarter 0), then the
-// quarter's buffer loads (at most two: a burst of them stalls instruction issue behind a full address queue), then
-// the MFMAs with kValu VALU ops after each and one A fragment read after every four; what remains (VALU, the LDS
-// store of a decoded block) goes last.
-template <int kB, int kLoads, int kValu>
+// Scheduling pattern for one quarter phase (kM MFMAs, one A fragment per four): the next phase's B fragment reads
+// first (quarter 0), then the quarter's buffer loads (at most two: a burst of them stalls instruction issue behind a
+// full address queue), then the MFMAs with kValu VALU ops after each and one A fragment read after every four; what
+// remains (VALU, the LDS store of a decoded block) goes last.
+template <int kM, int kB, int kLoads, int kValu>
 __device__ __forceinline__ void quarter_schedule() {
   constexpr int kMfma = 0x008, kValuM = 0x002, kVmem = 0x060, kDsRead = 0x100, kDsWrite = 0x200;
   if (kB) __builtin_amdgcn_sched_group_barrier(kDsRead, kB, 0);
   if (kLoads) __builtin_amdgcn_sched_group_barrier(kVmem, kLoads, 0);
 #pragma unroll
-  for (int g = 0; g < 8; g++) {
+  for (int g = 0; g < kM; g++) {
     __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
     if (kValu) __builtin_amdgcn_sched_group_barrier(kValuM, kValu, 0);
     if (g % 4 == 3) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
@@ -573,10 +574,13 @@ __device__ __forceinline__ void quarter_schedule() {
   __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
 }
 
-template <int G>
+template <int G, int MF>
 __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> args) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kAStage + 3 * kBStage];
-  uint8_t* const bl = lds + 2 * kAStage;
+  constexpr int TM = 32 * MF;                 // tile rows: MF 16-row fragments per wave, two waves down
+  constexpr int kAS = TM * BK * 2;            // bytes of one A stage
+  constexpr int kDma = (MF + 1) / 2;          // A loads of 8 rows per wave per stage
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kAS + 3 * kBStage];
+  uint8_t* const bl = lds + 2 * kAS;
 
   const int pid = xcd_remap(blockIdx.x, gridDim.x);
   int di = 0;
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   const int first_m = group * kGroupM;
   const int gm = min(d.tiles_m - first_m, kGroupM);
   const int in_group = local - group * kGroupM * d.tiles_n;
-  const int m0 = (first_m + in_group % gm) * BM;
+  const int m0 = (first_m + in_group % gm) * TM;
   const int n0 = (in_group / gm) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -633,34 +637,36 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   auto decode_store = [&](const u32x3& w, int r, uint8_t* stage) {
     *reinterpret_cast<bf16x8*>(stage + st_off0 + (8 * (r >> 1) + 2 * (r & 1)) * 2048) = decode_window(w.x, w.y, w.z, bo);
   };
-  // A: wave w fills rows 32 w .. +31 of a stage, 4 loads of 8 rows: load i covers row r = 32 w + lane / 8 + 8 i,
-  // 16-byte chunk (lane % 8) ^ swz(r). swz(r + 8) = swz(r) ^ 4, so loads 0, 2 and loads 1, 3 differ by 16 rows
-  // only: two offset registers, recomputed at each use (the empty asm hides their values from the compiler, which
-  // would otherwise keep four loop-invariant registers). Rows past M lie past the end of the buffer resource and
-  // read zeros.
-  const int ar0 = 32 * wave + (lane >> 3);
+  // A: a stage is TM / 8 loads of 8 rows (64 lanes x 16 bytes); wave w issues loads g = g0 + i (i < kDma), g0 =
+  // min(kDma w, TM / 8 - kDma) (a wave past the end repeats its neighbour's loads, which write the same bytes).
+  // Load g covers row r = 8 g + lane / 8, 16-byte chunk (lane % 8) ^ swz(r). swz(r + 8) = swz(r) ^ 4, so loads i
+  // and i + 2 differ by 16 rows only: two offset registers, recomputed at each use (the empty asm hides their values
+  // from the compiler, which would otherwise keep kDma loop-invariant registers). Rows past M lie past the end of
+  // the buffer resource and read zeros.
+  const int g0 = min(kDma * wave, TM / 8 - kDma);
+  const int ar0 = 8 * g0 + (lane >> 3);
   const uint32_t va_e = (uint32_t)(((int64_t)(m0 + ar0) * d.lda + ((lane & 7) ^ a_swz(ar0)) * 8) * 2);
   const uint32_t va_o = (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + ((lane & 7) ^ a_swz(ar0 + 8)) * 8) * 2);
   const uint32_t va_16 = (uint32_t)(16 * d.lda * 2);
   auto dma_a = [&](int stage, int k, int i) {
     uint32_t v = (i & 1) ? va_o : va_e;
     asm volatile("" : "+v"(v));
-    uint8_t* dst = lds + stage * kAStage + (32 * wave + 8 * i) * (BK * 2);
+    uint8_t* dst = lds + stage * kAS + 8 * (g0 + i) * (BK * 2);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16,
                                              v + (i >> 1) * va_16, k * BK * 2, 0, 0);
   };
-  f32x4 acc[8][4];
+  f32x4 acc[MF][4];
 #pragma unroll
-  for (int mf = 0; mf < 8; mf++)
+  for (int mf = 0; mf < MF; mf++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[mf][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int arow = lane & 15;
-  const uint32_t aoff0 = 128 * wm * (BK * 2) + arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
-  const uint32_t aoff1 = 128 * wm * (BK * 2) + arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
+  const uint32_t aoff0 = 16 * MF * wm * (BK * 2) + arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
+  const uint32_t aoff1 = 16 * MF * wm * (BK * 2) + arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
   const uint32_t boff = 4 * wn * 2048 + 16 * lane;
 
-  bf16x8 fa[8], fb0[4], fb1[4];
+  bf16x8 fa[MF], fb0[4], fb1[4];
   auto read_a = [&](const uint8_t* p, int mf) { return *reinterpret_cast<const bf16x8*>(p + mf * 16 * (BK * 2)); };
   auto read_b = [&](const uint8_t* p, int j) { return *reinterpret_cast<const bf16x8*>(p + j * 2048); };
 
@@ -668,7 +674,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   // and A(1) in flight; K half 0 of step 0 read into registers
   const int k1 = min(1, KT - 1);
 #pragma unroll
-  for (int i = 0; i < 4; i++) dma_a(0, 0, i);
+  for (int i = 0; i < kDma; i++) dma_a(0, 0, i);
   raw_a[0] = load_raw(0, 0); raw_a[1] = load_raw(1, 0);
   raw_b[0] = load_raw(2, 0); raw_b[1] = load_raw(3, 0);
   wait_vm<0>();
@@ -680,14 +686,15 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   // the loads in flight now are those of a phase 1, in its order, so the loop's wait counts hold on entry too
   raw_b[0] = load_raw(2, k1); raw_b[1] = load_raw(3, k1);
 #pragma unroll
-  for (int i = 0; i < 4; i++) dma_a(1, k1, i);
+  for (int i = 0; i < kDma; i++) dma_a(1, k1, i);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 4; j++) fb0[j] = read_b(bl + boff, j);
 #pragma unroll
-  for (int mf = 0; mf < 8; mf++) fa[mf] = read_a(lds + aoff0, mf);
+  for (int mf = 0; mf < MF; mf++) fa[mf] = read_a(lds + aoff0, mf);
 
-  // One phase of step k in four quarters of 8 MFMAs (scheduling fences between them). P = 0: MFMAs on K half 0 with
+  // One phase of step k in four quarters (fragments Q MF / 4 .. (Q + 1) MF / 4 - 1, scheduling fences between them).
+  // P = 0: MFMAs on K half 0 with
   // fb0, reads K half 1 of step k into fa / fb1, loads raw B(kl) blocks 0, 1 (quarters 0, 1), decodes raw B(k+1)
   // blocks 2, 3 into stage ds (quarters 0, 2). P = 1: MFMAs on K half 1 with fb1, reads K half 0 of step k+1 into
   // fa / fb0, loads raw B(kl) blocks 2, 3 (quarter 0) and DMAs A(kl) into A stage sa (quarters 1, 2), decodes raw
@@ -705,13 +712,14 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
       if constexpr (Q == 0) {
         raw_b[0] = load_raw(2, kl);
         raw_b[1] = load_raw(3, kl);
-      } else if constexpr (Q < 3) {
-        dma_a(sa, kl, 2 * (Q - 1));
-        dma_a(sa, kl, 2 * (Q - 1) + 1);
+      } else {
+        if constexpr (Q >= 1 && 2 * (Q - 1) < kDma) dma_a(sa, kl, 2 * (Q - 1));
+        if constexpr (Q >= 1 && 2 * (Q - 1) + 1 < kDma) dma_a(sa, kl, 2 * (Q - 1) + 1);
       }
     }
+    constexpr int lo = Q * MF / 4, hi = (Q + 1) * MF / 4;
 #pragma unroll
-    for (int mf = 2 * Q; mf < 2 * Q + 2; mf++) {
+    for (int mf = lo; mf < hi; mf++) {
 #pragma unroll
       for (int j = 0; j < 4; j++) acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mf], cur[j], acc[mf][j], 0, 0, 0);
       fa[mf] = read_a(na, mf);
@@ -722,8 +730,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
       else
         decode_store(raw_a[Q / 2], Q / 2, ds);
     }
-    constexpr int kL = P == 0 ? (Q < 2 ? 1 : 0) : (Q < 3 ? 2 : 0);
-    quarter_schedule<Q == 0 ? 4 : 0, kL, (Q == 0 || Q == 2) ? 3 : 0>();
+    constexpr int kDq = kDma - 2 * (Q - 1);  // A loads left for quarters Q >= 1
+    constexpr int kL = P == 0 ? (Q < 2 ? 1 : 0)
+                              : (Q == 0 ? 2 : (Q <= 2 ? (kDq < 0 ? 0 : (kDq > 2 ? 2 : kDq)) : 0));
+    quarter_schedule<4 * (hi - lo), Q == 0 ? 4 : 0, kL, (Q == 0 || Q == 2) ? 3 : 0>();
   };
   auto phase = [&]<int P>(bf16x8(&cur)[4], bf16x8(&nxt)[4], const uint8_t* na, const uint8_t* nb, uint8_t* ds, int kl,
                           int sa) {
@@ -738,11 +748,11 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   for (int k = 0; k < KT; k++) {
     const int sa0 = k & 1;
     const int kl = min(k + 2, KT - 1);
-    phase.template operator()<0>(fb0, fb1, lds + sa0 * kAStage + aoff1, bl + sb0 * kBStage + 1024 + boff,
+    phase.template operator()<0>(fb0, fb1, lds + sa0 * kAS + aoff1, bl + sb0 * kBStage + 1024 + boff,
                                  bl + sb1 * kBStage, kl, sa0);
     wait_vm<2>();  // A(k+1) done; raw B(k+2) blocks 0, 1 may stay in flight
     __syncthreads();
-    phase.template operator()<1>(fb1, fb0, lds + (sa0 ^ 1) * kAStage + aoff0, bl + sb1 * kBStage + boff,
+    phase.template operator()<1>(fb1, fb0, lds + (sa0 ^ 1) * kAS + aoff0, bl + sb1 * kBStage + boff,
                                  bl + sb2 * kBStage, kl, sa0);
     const int t = sb0;
     sb0 = sb1; sb1 = sb2; sb2 = t;
@@ -754,7 +764,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   // Bias and activation (and for SwiGLU the product silu(gate) * proj, whose operands share lane and register) are
   // applied in registers by all waves; the fp32 results are staged in LDS (row-quad layout, 128 KB) and finished
   // 8 columns at a time by all threads. SwiGLU stages the whole tile (256 rows x 128 output columns) at once, the
-  // other activations 128 rows x 256 columns per pass.
+  // other activations TM / 2 rows x 256 columns per pass.
   float* ep = reinterpret_cast<float*>(lds);
   const int col_in = lane & 15;
   const int nout = swiglu ? N / 2 : N;
@@ -768,16 +778,16 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
         const int tc = 16 * grp[jj] + col_in;
         const int c = ep_slot(64 * (tc >> 7) + (tc & 63));
 #pragma unroll
-        for (int mf = 0; mf < 8; mf++) {
+        for (int mf = 0; mf < MF; mf++) {
           f32x4 v;
 #pragma unroll
           for (int i = 0; i < 4; i++) v[i] = silu_f(acc[mf][jj][i] + bj[jj]) * (acc[mf][jj + 2][i] + bj[jj + 2]);
-          *reinterpret_cast<f32x4*>(ep + ((32 * wm + 4 * mf + (lane >> 4)) * 128 + c) * 4) = v;
+          *reinterpret_cast<f32x4*>(ep + ((4 * MF * wm + 4 * mf + (lane >> 4)) * 128 + c) * 4) = v;
         }
       }
     }
     __syncthreads();
-    ep8_finish<128>(d, ep, m0, n0 / 2, 64, nout, tid);
+    ep8_finish<128>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
   } else {
     const bool gelu = d.act == RL_ACT_GELU_TANH;
 #pragma unroll
@@ -787,7 +797,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
         for (int j = 0; j < 4; j++) {
           const int c = ep_slot(16 * grp[j] + col_in);
 #pragma unroll
-          for (int mf = 0; mf < 8; mf++) {
+          for (int mf = 0; mf < MF; mf++) {
             f32x4 v;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -799,7 +809,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
         }
       }
       __syncthreads();
-      ep8_finish<256>(d, ep, m0 + 128 * P, n0, 32, nout, tid);
+      ep8_finish<256>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
       __syncthreads();
     }
   }
@@ -838,12 +848,83 @@ static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, 
   return RL_OK;
 }
 
+// ---- launch planning for the 8-wave kernel ------------------------------------------------------------------------
+// Workgroups hold a whole CU (160 KB of LDS), so a launch of T tiles runs in ceil(T / CUs) rounds, each as long as one
+// tile: MF fragment rows per wave plus a part that does not shrink with the tile's rows (the B decode, prologue and
+// epilogue), about 1.5 fragments' worth. The planner picks the fragment count, and may run the rows past a multiple
+// of 256 as a second launch of shorter tiles, so that the last round is not a mostly idle full-height one.
+constexpr double kTileFixed = 1.5, kSecondLaunch = 1.0;
+constexpr int kMfChoices[] = {8, 7, 6, 4};
+
+static int64_t tiles8(int64_t M, int64_t N, int mf) { return ((M + 32 * mf - 1) / (32 * mf)) * ((N + BN - 1) / BN); }
+static double launch_cost(int64_t tiles, int mf, int cus) {
+  return (double)((tiles + cus - 1) / cus) * (mf + kTileFixed);
+}
+
+struct Plan8 {
+  int mf;         // fragments per wave of the (first) launch
+  int64_t split;  // rows of the first launch; 0 = a single launch over all rows
+  int mf_tail;    // fragments per wave of the second launch
+};
+
+static Plan8 plan8(int64_t M, int64_t N, int cus) {
+  Plan8 best{8, 0, 8};
+  double bc = 1e300;
+  for (int mf : kMfChoices) {
+    const double c = launch_cost(tiles8(M, N, mf), mf, cus);
+    if (c < bc) { bc = c; best = Plan8{mf, 0, mf}; }
+  }
+  for (int64_t R = 256; R < M; R += 256) {
+    const double c0 = launch_cost(tiles8(R, N, 8), 8, cus) + kSecondLaunch;
+    for (int mf : kMfChoices) {
+      const double c = c0 + launch_cost(tiles8(M - R, N, mf), mf, cus);
+      if (c < bc) { bc = c; best = Plan8{8, R, mf}; }
+    }
+  }
+  return best;
+}
+
+template <int G>
+static void set_tiles8(GemmArgs<G>& args, int mf, int& total) {
+  total = 0;
+  for (int i = 0; i < args.n; i++) {
+    GemmDesc& g = args.d[i];
+    g.tiles_m = (int32_t)((g.M + 32 * mf - 1) / (32 * mf));
+    g.tile_start = total;
+    total += g.tiles_m * g.tiles_n;
+  }
+  for (int i = args.n; i < G; i++) args.d[i] = args.d[args.n - 1];
+}
+
+template <int G>
+static int launch8(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(total_tiles), block(kG8Threads);
+  switch (mf) {
+    case 8: hipLaunchKernelGGL((gemm8_kernel<G, 8>), grid, block, 0, st, args); break;
+    case 7: hipLaunchKernelGGL((gemm8_kernel<G, 7>), grid, block, 0, st, args); break;
+    case 6: hipLaunchKernelGGL((gemm8_kernel<G, 6>), grid, block, 0, st, args); break;
+    default: hipLaunchKernelGGL((gemm8_kernel<G, 4>), grid, block, 0, st, args); break;
+  }
+  return launch_status("rl_bfp16_gemm");
+}
+
+// The descriptor of rows R.. of a GEMM.
+static GemmDesc rows_from(const GemmDesc& g, int64_t R) {
+  GemmDesc t = g;
+  t.A = static_cast<const uint16_t*>(g.A) + R * g.lda;
+  t.C = g.C + R * g.ldc;
+  if (g.res) t.res = g.res + R * g.ldr;
+  t.M = (int32_t)(g.M - R);
+  t.gate_split = (int32_t)(g.gate_split > R ? g.gate_split - R : 0);
+  return t;
+}
+
 template <int G>
 static int launch(const GemmArgs<G>& args, int total_tiles, int32_t a_fmt, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(total_tiles), block(kGThreads);
   switch (a_fmt) {
-    case RL_A_BF16: hipLaunchKernelGGL((gemm8_kernel<G>), grid, dim3(kG8Threads), 0, st, args); break;
     case RL_A_BF16_QUANTIZE: hipLaunchKernelGGL((gemm_kernel<RL_A_BF16_QUANTIZE, G>), grid, block, 0, st, args); break;
     case RL_A_PACKED_ROWBLOCK:
       hipLaunchKernelGGL((gemm_kernel<RL_A_PACKED_ROWBLOCK, G>), grid, block, 0, st, args);
@@ -865,7 +946,21 @@ int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_pa
   if (s) return s;
   args.n = 1;
   if ((s = check_device())) return s;
-  return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
+  if (a_fmt != RL_A_BF16) return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
+  const Plan8 p = plan8(M, N, device_cus());
+  int total = 0;
+  if (p.split == 0) {
+    set_tiles8(args, p.mf, total);
+    return launch8<1>(args, total, p.mf, stream);
+  }
+  GemmArgs<1> tail;
+  tail.d[0] = rows_from(args.d[0], p.split);
+  tail.n = 1;
+  args.d[0].M = (int32_t)p.split;
+  set_tiles8(args, p.mf, total);
+  if ((s = launch8<1>(args, total, p.mf, stream))) return s;
+  set_tiles8(tail, p.mf_tail, total);
+  return launch8<1>(tail, total, p.mf_tail, stream);
 }
 
 int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, void* stream) {
@@ -888,7 +983,19 @@ int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, v
   args.n = n;
   int s = check_device();
   if (s) return s;
-  return launch<RL_MAX_GROUP>(args, total, a_fmt, stream);
+  if (a_fmt != RL_A_BF16) return launch<RL_MAX_GROUP>(args, total, a_fmt, stream);
+  // one launch for the whole group, with the fragment count that minimises its rounds
+  const int cus = device_cus();
+  int best_mf = 8;
+  double bc = 1e300;
+  for (int mf : kMfChoices) {
+    int64_t t = 0;
+    for (int i = 0; i < n; i++) t += tiles8(args.d[i].M, args.d[i].N, mf);
+    const double c = launch_cost(t, mf, cus);
+    if (c < bc) { bc = c; best_mf = mf; }
+  }
+  set_tiles8(args, best_mf, total);
+  return launch8<RL_MAX_GROUP>(args, total, best_mf, stream);
 }
 
 }  // extern "C"

@@ -14,6 +14,8 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int ok();
 // RL_OK if the current device is a gfx950; caches the answer per device.
 int check_device();
+// Compute units of the current device (after check_device; 256 if unknown).
+int device_cus();
 // Converts a launch's HIP status into an RL status.
 int launch_status(const char* what);
 

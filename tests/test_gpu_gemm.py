@@ -165,3 +165,25 @@ def test_config1_full_size_rows(dev):
     np.testing.assert_array_equal(aq[torch.from_numpy(rows).cuda()].float().cpu().numpy(), Aq)
     Bq = F.decode_b(packed.cpu().numpy(), K, N)
     check(out[torch.from_numpy(rows).cuda()], G.gemm_ref(Aq, Bq))
+
+
+# Shapes that the launch planner of the bf16 path (256 CUs) runs with 6, 7 and 8 fragment rows per wave (192-, 224-
+# and 256-row tiles), and as a 256-row-tile launch over the first 4096 rows followed by a 128-row-tile launch over
+# the rest. Checked on sampled rows (the first and last tiles and both sides of every tile boundary near the split).
+@pytest.mark.parametrize("M,N", [(3072, 4096), (4352, 3072), (4096, 4096), (4352, 24576)])
+def test_tile_plans(dev, M, N):
+    K = 64
+    rng, A, packed, Aq, Bq = setup(M, K, N, M + N)
+    res = F.bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    gate = rng.standard_normal((2, N)).astype(np.float32)
+    split = 4100  # gate row 1 for rows below; lies in the second launch for M = 4352, N = 24576
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, gate=dev_t(gate, torch.float32),
+                   gate_split_row=split, residual=dev_t(res, torch.bfloat16))
+    rows = np.unique(np.concatenate([np.arange(0, 20), np.arange(M - 20, M), np.arange(4090, min(M, 4110)),
+                                     np.arange(180, 200), np.arange(215, 235), np.arange(250, 262),
+                                     rng.integers(0, M, 64)]))
+    rows = rows[rows < M]
+    # gate row 1 applies to global rows below the split: evaluate the sampled rows with each gate row and select
+    ref = np.where((rows < split)[:, None], G.gemm_ref(Aq[rows], Bq, gate=gate[[1, 1]], residual=res[rows]),
+                   G.gemm_ref(Aq[rows], Bq, gate=gate[[0, 0]], residual=res[rows]))
+    check(out[torch.from_numpy(rows).cuda()], ref)

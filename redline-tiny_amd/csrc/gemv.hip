@@ -38,7 +38,9 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv
   constexpr int S = 2;  // register slots: one iteration in flight while the other is used
   __shared__ __attribute__((aligned(16))) uint8_t buf[kVWaves][kVIterBytes];
   __shared__ float red[kVWaves][M][16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index is uniform across the wave: readfirstlane puts it (and the load offsets built from it) in scalar
+  // registers, as buffer loads need
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KT = K / 64;
   const int iters = (KT + 7) / 8;
   const int mine = wave < iters ? (iters - wave + kVWaves - 1) / kVWaves : 0;  // this wave's iterations

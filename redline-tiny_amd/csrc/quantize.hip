@@ -75,8 +75,23 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const void* __restr
     }
     const uint32_t E = block_exp(u);
     int32_t q[8];
+    uint32_t b[8];
+    if (E >= 7u && E <= 254u) {
+      // powers of two scale exactly and v_rndne rounds half to even, so this equals the integer encoder; for these
+      // exponents every scaled value and every decoded value is a normal float
 #pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = encode_elem(u[i], E);
+      for (int i = 0; i < 8; i++) {
+        const float qf = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(__uint_as_float(u[i]), 133 - (int)E)), 127.0f);
+        q[i] = (int32_t)qf;
+        b[i] = __float_as_uint(__builtin_amdgcn_ldexpf(qf, (int)E - 133) + 0.0f) >> 16;  // exact in bf16; -0 -> +0
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        q[i] = encode_elem(u[i], E);
+        b[i] = decode_bf16_bits(q[i], E);
+      }
+    }
     if (packed) {
       uint8_t* s = stage + threadIdx.x * kBlockBytes;
       s[0] = (uint8_t)E;
@@ -84,9 +99,6 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const void* __restr
       for (int i = 0; i < 8; i++) s[1 + i] = (uint8_t)(int8_t)q[i];
     }
     if (deq) {
-      uint32_t b[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) b[i] = decode_bf16_bits(q[i], E);
       u32x4 o;
       o.x = b[0] | (b[1] << 16); o.y = b[2] | (b[3] << 16); o.z = b[4] | (b[5] << 16); o.w = b[6] | (b[7] << 16);
       *reinterpret_cast<u32x4*>(deq + r * cols + cb * 8) = o;

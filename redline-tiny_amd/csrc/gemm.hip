@@ -530,14 +530,15 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
 }
 
 // ---- 8-wave kernel for bf16 A ---------------------------------------------------------------------------------
-// Same 256 x 256 tile and K steps of 64, with 8 waves: one SIMD's MFMA pipe only stays full with two waves issuing.
-// Wave (wm, wn) = (w / 4, w % 4) owns rows 128 wm .. +127 and the four 16-column groups in B slots 4 wn .. 4 wn + 3:
-// 8 x 4 MFMA accumulators.
+// Tiles of 32 MF rows x 256 columns (MF = 8: 256 x 256) and K steps of 64, with 8 waves: one SIMD's MFMA pipe only
+// stays full with two waves issuing. Wave (wm, wn) = (w / 4, w % 4) owns rows 16 MF wm .. +16 MF - 1 and the four
+// 16-column groups in B slots 4 wn .. 4 wn + 3: MF x 4 MFMA accumulators.
 //
-// LDS (160 KB): two A stages (256 x 64 bf16 with the 16-byte chunk swizzle, filled by direct-to-LDS buffer loads)
-// and three B stages. A B stage holds the 2048 decoded blocks of the tile's two b_layout tiles, 16 bytes each, in
-// MFMA operand order: slot s is one 16-column group x 64 K as two 1 KB fragments (K half h at 1024 h, lane l = block
-// l). Groups are put in slots at decode time so that each wave's four groups are adjacent (for SwiGLU, gate groups
+// LDS (up to 160 KB): two A stages (tile rows x 64 bf16 with the 16-byte chunk swizzle, filled by direct-to-LDS
+// buffer loads) and three B stages. A B stage holds the 2048 decoded blocks of the tile's two b_layout tiles, 16
+// bytes each, as MFMA operands: slot s is one 16-column group x 64 K as two 1 KB fragments (K half h at 1024 h; lane
+// l's block l at 16 frag_pos(l)). Groups are put in slots at decode time so that each wave's four groups are
+// adjacent (for SwiGLU, gate groups
 // {g, g+1} and proj groups {g+4, g+5} of one 128-column tile, so silu(gate) * proj pairs share lane and register).
 //
 // A K step is two phases, one per 32-deep half of K (32 MFMAs per wave). The operands of a phase are read into
@@ -553,6 +554,12 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
 // and land in stages that are never read again.
 constexpr int kG8Threads = 512;
 constexpr int kBStage = 2 * 1024 * 16;  // decoded blocks of two 64 x 128 tiles, 16 bytes each
+
+// Position of block m (0..63) of a decoded B fragment inside its 1 KB: a 4 x 4 transpose within each group of 16
+// blocks, with bit 2 flipped in odd groups.
+__device__ __forceinline__ int frag_pos(int m) {
+  return (m & ~15) | ((((m & 3) * 4 + ((m >> 2) & 3)) ^ (((m >> 4) & 1) * 4)));
+}
 static_assert(2 * kAStage + 3 * kBStage <= 160 * 1024, "LDS budget");
 
 // Scheduling pattern for one quarter phase (kM MFMAs, one A fragment per four): the next phase's B fragment reads
@@ -618,24 +625,52 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
       (void*)d.A, (short)0, (int)(((int64_t)d.M - 1) * d.lda * 2 + (int64_t)d.K * 2), 0x00020000);
 
-  // B decode: thread t decodes blocks b = t + 512 r (r = 0..3) of the two tiles: tile h = r / 2, block bi = t +
-  // 512 (r % 2) in it, i.e. column group c = bi / 128, K half bi / 64 % 2, operand lane bi % 64. Its raw window
-  // starts at 9 bi rounded down to 4 bytes (offset t % 4 inside). The second tile's windows read zeros (offset past
-  // the stream, outside the range check) when it lies beyond N; its decode is never read.
+  // B decode: thread t decodes the 4 consecutive blocks bi = 4 u .. 4 u + 3 (u = t % 256) of tile h = t / 256, a
+  // 36-byte dword-aligned run at byte 36 u of the tile, so every byte's position is known at compile time. The run
+  // is read as two halves of 5 dwords (blocks 0, 1: dwords 0..4; blocks 2, 3: dwords 4..8), each a 16-byte and a
+  // 4-byte load. The blocks share column group c = u / 32 and K half u / 16 % 2 and are operand lanes 4 (u % 16)
+  // + j of that fragment. The second tile reads zeros (offset past the stream, outside the range
+  // check) when it lies beyond N; its decode is never read.
   const int64_t nt0 = n0 >> 7;
-  const uint32_t vb0 = (uint32_t)(nt0 * KT * kTileBytes + ((9 * tid) & ~3));
-  const uint32_t vb1 = nt0 + 1 < (N >> 7) ? (uint32_t)((nt0 + 1) * KT * kTileBytes + ((9 * tid) & ~3)) : 0x7FFFFFF0u;
-  const uint32_t bo = tid & 3;
-  // LDS byte offset of block r inside a B stage: group G = 8 h + c goes to slot 4 (2 h + c / 2 % 2) + 2 (c / 4) +
-  // c % 2, so block r sits at st_off0 + (8 h + 2 (r % 2)) * 2048 (c = t / 128 + 4 (r % 2), h = r / 2)
-  const uint32_t st_off0 = (4 * ((tid >> 8) & 1) + ((tid >> 7) & 1)) * 2048 + ((tid >> 6) & 1) * 1024 + 16 * lane;
-  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-  u32x3 raw_a[2], raw_b[2];  // blocks r = 0, 1 and r = 2, 3
-  auto load_raw = [&](int r, int k) {
-    return __builtin_amdgcn_raw_buffer_load_b96(brs, r >= 2 ? vb1 : vb0, k * kTileBytes + (r & 1) * 9 * 512, 0);
+  const int bh = tid >> 8, bu = tid & 255;
+  const uint32_t vb = nt0 + bh < (N >> 7) ? (uint32_t)((nt0 + bh) * KT * kTileBytes + 36 * bu) : 0x7FFFFFF0u;
+  // group G = 8 h + c goes to LDS slot 4 (2 h + c / 2 % 2) + 2 (c / 4) + c % 2. Inside a 1 KB fragment, block m sits
+  // at position frag_pos(m) (a 4 x 4 transpose in each 16 blocks, bit 2 flipped in odd 16s), not m: measured on
+  // gfx950, this keeps both the operand reads (lane m reads block m) and the decode stores (store J: lane a writes
+  // block 4 a + J; a 16-byte-per-lane store is served 8 lanes at a time, which must hit distinct 16-byte slots of
+  // a 128-byte line) free of bank conflicts, where the plain order makes the stores 4-way conflicted.
+  const int bc = bu >> 5, ba = bu & 15;
+  uint32_t st_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    st_off[j] = (4 * (2 * bh + ((bc >> 1) & 1)) + 2 * (bc >> 2) + (bc & 1)) * 2048 + ((bu >> 4) & 1) * 1024 +
+                16 * frag_pos(4 * ba + j);
+  struct RawHalf {
+    u32x4 v;
+    uint32_t w;
   };
-  auto decode_store = [&](const u32x3& w, int r, uint8_t* stage) {
-    *reinterpret_cast<bf16x8*>(stage + st_off0 + (8 * (r >> 1) + 2 * (r & 1)) * 2048) = decode_window(w.x, w.y, w.z, bo);
+  RawHalf raw_a, raw_b;  // the run's first (blocks 0, 1) and second (blocks 2, 3) half
+  // part 0: the half's first 4 dwords, part 1: its fifth
+  auto load_part = [&](RawHalf& r, int half, int part, int k) {
+    if (part == 0)
+      r.v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, vb, k * kTileBytes + 16 * half, 0));
+    else
+      r.w = __builtin_amdgcn_raw_buffer_load_b32(brs, vb, k * kTileBytes + 16 * half + 16, 0);
+  };
+  // block j (0..3) of the run from its half: E at byte 9 j, q at bytes 9 j + 1 .. 9 j + 8, byte b of the run in
+  // dword b / 4 - 4 half of the half
+  auto decode_store = [&]<int J>(const RawHalf& r, uint8_t* stage) {
+    const uint32_t d[5] = {r.v.x, r.v.y, r.v.z, r.v.w, r.w};
+    constexpr int base = 16 * (J / 2);
+    auto sbyte = [&](int b) { return (float)(int8_t)(d[(b - base) >> 2] >> (8 * ((b - base) & 3))); };
+    constexpr int e = 9 * J;
+    const float sc = block_scale((d[(e - base) >> 2] >> (8 * ((e - base) & 3))) & 0xFFu);
+    u32x4 o;
+    o.x = pack_hi(sbyte(e + 1) * sc, sbyte(e + 2) * sc);
+    o.y = pack_hi(sbyte(e + 3) * sc, sbyte(e + 4) * sc);
+    o.z = pack_hi(sbyte(e + 5) * sc, sbyte(e + 6) * sc);
+    o.w = pack_hi(sbyte(e + 7) * sc, sbyte(e + 8) * sc);
+    *reinterpret_cast<u32x4*>(stage + st_off[J]) = o;
   };
   // A: a stage is TM / 8 loads of 8 rows (64 lanes x 16 bytes); wave w issues loads g = g0 + i (i < kDma), g0 =
   // min(kDma w, TM / 8 - kDma) (a wave past the end repeats its neighbour's loads, which write the same bytes).
@@ -664,7 +699,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   const int arow = lane & 15;
   const uint32_t aoff0 = 16 * MF * wm * (BK * 2) + arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
   const uint32_t aoff1 = 16 * MF * wm * (BK * 2) + arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
-  const uint32_t boff = 4 * wn * 2048 + 16 * lane;
+  const uint32_t boff = 4 * wn * 2048 + 16 * frag_pos(lane);
 
   bf16x8 fa[MF], fb0[4], fb1[4];
   auto read_a = [&](const uint8_t* p, int mf) { return *reinterpret_cast<const bf16x8*>(p + mf * 16 * (BK * 2)); };
@@ -675,16 +710,16 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   const int k1 = min(1, KT - 1);
 #pragma unroll
   for (int i = 0; i < kDma; i++) dma_a(0, 0, i);
-  raw_a[0] = load_raw(0, 0); raw_a[1] = load_raw(1, 0);
-  raw_b[0] = load_raw(2, 0); raw_b[1] = load_raw(3, 0);
+  load_part(raw_a, 0, 0, 0); load_part(raw_a, 0, 1, 0);
+  load_part(raw_b, 1, 0, 0); load_part(raw_b, 1, 1, 0);
   wait_vm<0>();
-  decode_store(raw_a[0], 0, bl); decode_store(raw_a[1], 1, bl);
-  decode_store(raw_b[0], 2, bl); decode_store(raw_b[1], 3, bl);
-  raw_a[0] = load_raw(0, k1); raw_a[1] = load_raw(1, k1);
+  decode_store.template operator()<0>(raw_a, bl); decode_store.template operator()<1>(raw_a, bl);
+  decode_store.template operator()<2>(raw_b, bl); decode_store.template operator()<3>(raw_b, bl);
+  load_part(raw_a, 0, 0, k1); load_part(raw_a, 0, 1, k1);
   wait_vm<0>();
-  decode_store(raw_a[0], 0, bl + kBStage); decode_store(raw_a[1], 1, bl + kBStage);
+  decode_store.template operator()<0>(raw_a, bl + kBStage); decode_store.template operator()<1>(raw_a, bl + kBStage);
   // the loads in flight now are those of a phase 1, in its order, so the loop's wait counts hold on entry too
-  raw_b[0] = load_raw(2, k1); raw_b[1] = load_raw(3, k1);
+  load_part(raw_b, 1, 0, k1); load_part(raw_b, 1, 1, k1);
 #pragma unroll
   for (int i = 0; i < kDma; i++) dma_a(1, k1, i);
   __syncthreads();
@@ -707,11 +742,11 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
       for (int j = 0; j < 4; j++) nxt[j] = read_b(nb, j);
     }
     if constexpr (P == 0) {
-      if constexpr (Q < 2) raw_a[Q] = load_raw(Q, kl);
+      if constexpr (Q < 2) load_part(raw_a, 0, Q, kl);
     } else {
       if constexpr (Q == 0) {
-        raw_b[0] = load_raw(2, kl);
-        raw_b[1] = load_raw(3, kl);
+        load_part(raw_b, 1, 0, kl);
+        load_part(raw_b, 1, 1, kl);
       } else {
         if constexpr (Q >= 1 && 2 * (Q - 1) < kDma) dma_a(sa, kl, 2 * (Q - 1));
         if constexpr (Q >= 1 && 2 * (Q - 1) + 1 < kDma) dma_a(sa, kl, 2 * (Q - 1) + 1);
@@ -726,9 +761,9 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
     }
     if constexpr (Q == 0 || Q == 2) {
       if constexpr (P == 0)
-        decode_store(raw_b[Q / 2], 2 + Q / 2, ds);
+        decode_store.template operator()<2 + Q / 2>(raw_b, ds);
       else
-        decode_store(raw_a[Q / 2], Q / 2, ds);
+        decode_store.template operator()<Q / 2>(raw_a, ds);
     }
     constexpr int kDq = kDma - 2 * (Q - 1);  // A loads left for quarters Q >= 1
     constexpr int kL = P == 0 ? (Q < 2 ? 1 : 0)

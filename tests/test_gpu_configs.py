@@ -1,0 +1,127 @@
+"""The configurations of the reference's GEMM path at their full sizes (seed 0, the draw order activations,
+weights, epilogue vectors): the GPU result on sampled rows against the emulation (decoded operands, float64
+products, the fused epilogue, bf16), the grouped launch bit-identical to single launches, and the packed H of the
+FFN pair re-encoding to itself (but for the -128 corner). Weights are packed on the GPU (byte-identical to the CPU packer, checked in
+test_gpu_quantize.py) and decoded on the CPU for the reference."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bfp16 as F
+from oracle import gemm as G
+from rlbfp import ops
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def cuda(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda().to(dtype)
+
+
+def sample_rows(rng, M, n=48):
+    """Rows at both ends, around the 128/224/256-row tile boundaries and the 4096-row launch split, and random."""
+    edges = [0, 1, 127, 128, 223, 224, 255, 256, 4095, 4096, M - 129, M - 128, M - 1]
+    rows = np.concatenate([np.array([r for r in edges if 0 <= r < M]), rng.integers(0, M, n)])
+    return np.unique(rows)
+
+
+def check_rows(out, rows, ref):
+    got = out[torch.from_numpy(rows).cuda()].float().cpu().numpy()
+    err = G.rel_err(got, ref)
+    assert err <= TOL, f"rel err {err}"
+    d = np.abs(got.astype(np.float64) - ref)
+    assert (d <= 2 * np.abs(ref) * 2.0 ** -8 + 1e-4 * np.abs(ref).max()).mean() > 0.999
+
+
+def packed_weight(rng, N, K):
+    W = G.linear_weight(rng, N, K)
+    p = ops.pack_weight(cuda(W, torch.float32))
+    return p, F.decode_b(p.cpu().numpy(), K, N)
+
+
+def packed_up(rng, F_, K):
+    wg, wp = G.linear_weight(rng, F_, K), G.linear_weight(rng, F_, K)
+    p = ops.pack_weight(ops.interleave_up(cuda(wg, torch.float32), cuda(wp, torch.float32)))
+    return p, F.decode_b(p.cpu().numpy(), K, 2 * F_)
+
+
+def test_config2_qkv_bias_outliers(dev):
+    """DiT joint-attention QKV: M=4352, K=3072, N=9216, 1% of channels x20, bias epilogue; quantize-on-load and the
+    separate quantize pass give identical results."""
+    rng = np.random.default_rng(0)
+    M, K, N = 4352, 3072, 9216
+    A = G.activations(rng, M, K, outliers=0.01)
+    bw, Bq = packed_weight(rng, N, K)
+    bias = (rng.standard_normal(N) * 0.02).astype(np.float32)
+    a = cuda(A, torch.bfloat16)
+    _, aq = ops.quantize(a, deq=True)
+    out = ops.gemm(aq, bw, N, K, bias=cuda(bias, torch.float32))
+    out_q = ops.gemm(a, bw, N, K, a_fmt="bf16_quantize", bias=cuda(bias, torch.float32))
+    assert torch.equal(out, out_q)
+    rows = sample_rows(rng, M)
+    check_rows(out, rows, G.gemm_ref(F.quantize_rows(A[rows]), Bq, bias=bias))
+
+
+def test_config3_ffn_pair(dev):
+    """DiT FFN pair: up 4352x3072x(2x12288) SwiGLU with re-quantized H, then down 4352x12288x3072 with gate and
+    residual; the down GEMM is checked on the GPU's own H rows."""
+    rng = np.random.default_rng(0)
+    M, K, FF = 4352, 3072, 12288
+    X = G.activations(rng, M, K)
+    up, Bup = packed_up(rng, FF, K)
+    down, Bdown = packed_weight(rng, K, FF)
+    res = F.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    gate = rng.standard_normal(K).astype(np.float32)
+    _, xq = ops.quantize(cuda(X, torch.bfloat16), deq=True)
+    h = ops.gemm(xq, up, 2 * FF, K, act="swiglu", quantize_out=True)
+    out = ops.gemm(h, down, K, FF, gate=cuda(gate, torch.float32), residual=cuda(res, torch.bfloat16))
+    rows = sample_rows(rng, M, n=24)
+    check_rows(h, rows, G.gemm_ref(F.quantize_rows(X[rows]), Bup, act=G.ACT_SWIGLU, quantize_out=True))
+    H = h[torch.from_numpy(rows).cuda()].float().cpu().numpy()
+    # H is made of bfp16 blocks: re-encoding changes nothing but the -128 corner (a block whose largest magnitude
+    # is -2^k re-encodes one exponent up)
+    blocks = H.reshape(-1, 8).astype(np.float64)
+    same = (F.quantize_rows(H).reshape(-1, 8) == blocks).all(1)
+    vmax = blocks[np.arange(len(blocks)), np.abs(blocks).argmax(1)]
+    corner = (vmax < 0) & (np.frexp(-vmax)[0] == 0.5)
+    assert same[~corner].all()
+    check_rows(out, rows, G.gemm_ref(H, Bdown, gate=gate, residual=res[rows]))
+
+
+def test_config4_text_encoder_mlp(dev):
+    """Text-encoder prefill MLP: M=512 RMS-normalised rows, up K=4096 N=2x12288 SwiGLU, down K=12288 N=4096."""
+    rng = np.random.default_rng(0)
+    M, K, FF = 512, 4096, 12288
+    X = G.activations(rng, M, K, rms_rows=True)
+    up, Bup = packed_up(rng, FF, K)
+    down, Bdown = packed_weight(rng, K, FF)
+    _, xq = ops.quantize(cuda(X, torch.bfloat16), deq=True)
+    h = ops.gemm(xq, up, 2 * FF, K, act="swiglu", quantize_out=True)
+    out = ops.gemm(h, down, K, FF)
+    rows = sample_rows(rng, M, n=24)
+    check_rows(h, rows, G.gemm_ref(F.quantize_rows(X[rows]), Bup, act=G.ACT_SWIGLU, quantize_out=True))
+    check_rows(out, rows, G.gemm_ref(h[torch.from_numpy(rows).cuda()].float().cpu().numpy(), Bdown))
+
+
+def test_config5_grouped_streams(dev):
+    """One DiT block at 1024x1024: the image (M=4096) and text (M=256) streams' QKV projections with separate
+    weights as one grouped launch, identical to two single launches; the modulation GEMV at M=1, K=3072, N=18432."""
+    rng = np.random.default_rng(0)
+    K, N = 3072, 9216
+    streams = []
+    for M in (4096, 256):
+        A = G.activations(rng, M, K)
+        bw, Bq = packed_weight(rng, N, K)
+        _, aq = ops.quantize(cuda(A, torch.bfloat16), deq=True)
+        streams.append((M, A, bw, Bq, aq))
+    outs = ops.gemm_grouped([ops.GemmSpec(aq, bw, N, K) for (_, _, bw, _, aq) in streams])
+    for (M, A, bw, Bq, aq), o in zip(streams, outs):
+        assert torch.equal(o, ops.gemm(aq, bw, N, K))
+        rows = sample_rows(rng, M, n=16)
+        check_rows(o, rows, G.gemm_ref(F.quantize_rows(A[rows]), Bq))
+    temb = F.bf16_round(rng.standard_normal((1, K)).astype(np.float32))
+    wm, Bm = packed_weight(rng, 6 * K, K)
+    y = ops.gemv(cuda(temb, torch.bfloat16), wm, 6 * K, act="silu")
+    assert G.rel_err(y.float().cpu().numpy(), G.gemv_ref(temb, Bm)) <= TOL

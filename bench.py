@@ -15,7 +15,7 @@ Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s ag
 rotating weight copies so that the 256 MB MALL cannot hold them, and the CPU baseline (the oracle's numpy restatement
 of the reference CPU path on a row sample of the same workload).
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--copy-probe MB] [--sustain SECONDS]
 """
 
 import argparse
@@ -255,18 +255,94 @@ def copy_probe(mb, reps=10):
                       "gbps_rw": round(2 * n / us / 1e3, 1)}), flush=True)
 
 
+def _smi_sample():
+    """One `amd-smi metric -p -c` reading of GPU 0: (socket power W, mean graphics clock MHz over the XCDs), or
+    (None, None) when the tool is absent or prints something else."""
+    import re
+    import subprocess
+    try:
+        txt = subprocess.run(["amd-smi", "metric", "-p", "-c", "-g", "0"], capture_output=True, text=True,
+                             timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None, None
+    pw = re.search(r"SOCKET_POWER:\s*([0-9.]+)\s*W", txt)
+    clks = [float(c) for c in re.findall(r"GFX_\d+:\s*\n\s*CLK:\s*([0-9.]+)\s*MHz", txt)]
+    return (float(pw.group(1)) if pw else None), (sum(clks) / len(clks) if clks else None)
+
+
+def sustain(seconds):
+    """Runs the up GEMM back to back for `seconds`, then torch's bf16 linear of the same shape (hipBLASLt, no decode,
+    no epilogue) for as long, while a thread reads socket power and graphics clock with amd-smi. One JSON line per
+    kernel: time per call and the power/clock readings taken while it ran."""
+    import threading
+
+    import torch
+
+    from rlbfp import ops
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+    w_up = torch.randn((2 * FF, K), generator=g, device=dev) * 0.02
+    packed = ops.pack_weight(ops.interleave_up(w_up[:FF], w_up[FF:]))
+    a_q = ops.quantize(a, deq=True)[1]
+    h = torch.empty((M, FF), dtype=torch.bfloat16, device=dev)
+    w_bf = w_up.to(torch.bfloat16)
+    runs = {"gemm8 up GEMM + SwiGLU (bfp16 weights)":
+            lambda: ops.gemm(a_q, packed, 2 * FF, K, act="swiglu", quantize_out=True, out=h),
+            "torch bf16 linear, same shape": lambda: torch.nn.functional.linear(a_q, w_bf)}
+    for name, fn in runs.items():
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        samples, stop = [], threading.Event()
+
+        def sampler():
+            time.sleep(min(1.0, seconds / 4))  # past the first launches
+            while not stop.is_set():
+                samples.append(_smi_sample())
+                time.sleep(0.25)
+
+        th = threading.Thread(target=sampler)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n, t0 = 0, time.time()
+        th.start()
+        e0.record()
+        while time.time() - t0 < seconds:
+            for _ in range(100):
+                fn()
+            n += 100
+            torch.cuda.synchronize()
+        e1.record()
+        torch.cuda.synchronize()
+        stop.set()
+        th.join()
+        pw = [p for p, _ in samples if p is not None]
+        ck = [c for _, c in samples if c is not None]
+        print(json.dumps({"sustain": name, "shape": [M, K, 2 * FF], "calls": n,
+                          "us_per_call": round(e0.elapsed_time(e1) * 1e3 / n, 2),
+                          "tflops": round(flops_up() * n / (e0.elapsed_time(e1) * 1e-3) / 1e12, 1),
+                          "socket_power_w": pw, "gfx_clock_mhz": [round(c) for c in ck]}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sustain", type=float, default=0, metavar="SECONDS",
+                    help="only run the up GEMM, then torch's bf16 linear of the same shape, back to back for SECONDS "
+                         "each while amd-smi reads socket power and graphics clock; print one line per kernel and exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run device-to-device copies of MB megabytes (calibrates rocprofv3 FETCH_SIZE and "
                          "WRITE_SIZE against a transfer of known size), print their bandwidth and exit")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe(args.copy_probe)
+        return
+    if args.sustain:
+        sustain(args.sustain)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by weight columns, "

@@ -125,8 +125,35 @@ enum { RL_GEMV_SILU = 3 };
 int rl_bfp16_gemv(const uint16_t *x, int64_t ldx, const uint8_t *B_packed, uint16_t *y, int64_t ldy, int64_t M,
                   int64_t N, int64_t K, int32_t act, void *stream);
 
+/* ---- residual add + LayerNorm / RMSNorm + modulate -> the next GEMM's A ----------------------------------------
+ * For each row r of (M, D):
+ *   x'[r] = bf16(x[r] + g * branch[r])   one fp32 fma, then RNE; branch NULL means 0;
+ *   y[r]  = (x'[r] - mean) * rstd * sc   fp32; RL_NORM_LAYER: mean and variance of the row's D values of x' (eps
+ *                                        1e-6, no affine); RL_NORM_RMS: mean = 0, rstd = 1 / sqrt(mean(x'^2) + 1e-6);
+ * then y is quantized to bfp16 blocks of 8 along the row (as rl_bfp16_quantize does).
+ * g and sc come from params, (2, 2D) bf16 with row p = [g (D) | sc (D)] (run_ln.ln_params, redline/run_ln.py:38-40;
+ * vlm_run.rms_params, redline/vlm_run.py:62-65). Rows r < split_row use params row 1, the rest row 0
+ * (run_ln.rows_param, redline/run_ln.py:82-86; the reference's S is split_row / 128).
+ * The branch is bf16 row major (ld_br), or bfp16 packed in RL_ORDER_ROWBLOCK of (M, D) (ld_br ignored).
+ * Outputs (each may be NULL, not all three):
+ *   x_out: x' as bf16 row major (ld_xo); may equal x;
+ *   a_packed: 9*M*D/8 bytes of y in a_order (RL_ORDER_ROWBLOCK, or RL_ORDER_A_LAYOUT with M % 128 == 0);
+ *   a_deq: y's bfp16 values as bf16, row major (ld_a), the next rl_bfp16_gemm's RL_A_BF16 operand.
+ * D % 64 == 0 and 64 <= D <= 8192.
+ * Replaces the fused residual + LayerNorm + modulate artifact, kernels/glue/ln_design.py:38-118 with ln_mod.cc:92-204,
+ * run by run_ln.ln_run (redline/run_ln.py:43-57). With RL_NORM_RMS it replaces its RMSNorm copies
+ * (kernels/vlm/rms_mod.cc, rms16_mod.cc for a bf16 branch) run by LM._rms (redline/vlm_run.py:343-344). */
+enum { RL_NORM_LAYER = 0, RL_NORM_RMS = 1 };
+enum { RL_BRANCH_BF16 = 0, RL_BRANCH_PACKED = 1 };
+int rl_ln_modulate(const uint16_t *x, int64_t ldx, const void *branch, int32_t br_fmt, int64_t ld_br,
+                   const uint16_t *params, int64_t split_row, int32_t norm, uint16_t *x_out, int64_t ld_xo,
+                   uint8_t *a_packed, int32_t a_order, uint16_t *a_deq, int64_t ld_a, int64_t M, int64_t D,
+                   void *stream);
+
 /* ---- host-only helpers (no GPU needed) ---------------------------------------------------------------------------- */
 /* Shape/argument checks the entry points run before launching, callable on a machine without a GPU. */
+int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int64_t ld_xo, int32_t a_order,
+                   int64_t ld_a, int64_t split_row, int64_t M, int64_t D);
 int rl_validate_quantize(int32_t x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int32_t order);
 int rl_validate_gemm(int32_t a_fmt, int64_t lda, int64_t ldc, int64_t M, int64_t N, int64_t K, const rl_epilogue *ep);
 int rl_validate_gemv(int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t act);

@@ -139,4 +139,25 @@ int rl_validate_gemv(int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, 
   return rl::ok();
 }
 
+int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int64_t ld_xo, int32_t a_order,
+                   int64_t ld_a, int64_t split_row, int64_t M, int64_t D) {
+  using rl::fail;
+  if (M < 1 || M > (1 << 30) || D < 64 || D > 8192 || D % 64)
+    return fail(RL_ERR_SHAPE, "M %lld D %lld: need M >= 1, D %% 64 == 0, 64 <= D <= 8192", (long long)M,
+                (long long)D);
+  if (norm != RL_NORM_LAYER && norm != RL_NORM_RMS) return fail(RL_ERR_ARG, "norm %d unknown", norm);
+  if (br_fmt != RL_BRANCH_BF16 && br_fmt != RL_BRANCH_PACKED) return fail(RL_ERR_ARG, "br_fmt %d unknown", br_fmt);
+  if (a_order != RL_ORDER_ROWBLOCK && a_order != RL_ORDER_A_LAYOUT)
+    return fail(RL_ERR_ARG, "a_order %d: RL_ORDER_ROWBLOCK or RL_ORDER_A_LAYOUT", a_order);
+  if (a_order == RL_ORDER_A_LAYOUT && M % 128)
+    return fail(RL_ERR_SHAPE, "a_order A_LAYOUT needs M %% 128 == 0 (got %lld)", (long long)M);
+  if (split_row < 0) return fail(RL_ERR_ARG, "split_row < 0");
+  if (ldx < D || ldx % 8) return fail(RL_ERR_ALIGN, "ldx %lld: need >= D and a multiple of 8", (long long)ldx);
+  if (br_fmt == RL_BRANCH_BF16 && (ld_br < D || ld_br % 8))
+    return fail(RL_ERR_ALIGN, "ld_br %lld: need >= D and a multiple of 8", (long long)ld_br);
+  if (ld_xo < D || ld_xo % 8) return fail(RL_ERR_ALIGN, "ld_xo %lld: need >= D and a multiple of 8", (long long)ld_xo);
+  if (ld_a < D || ld_a % 8) return fail(RL_ERR_ALIGN, "ld_a %lld: need >= D and a multiple of 8", (long long)ld_a);
+  return rl::ok();
+}
+
 }  // extern "C"

@@ -506,7 +506,6 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
   // re-quantizing), applies the epilogue in fp32 and writes 16 bytes of bf16 per row.
   float* ep = reinterpret_cast<float*>(lds);
   const int col_in = lane & 15;
-  const int row_in = 4 * (lane >> 4);
   const bool swiglu = d.act == RL_ACT_SWIGLU;
   const int nout = swiglu ? N / 2 : N;
   auto pass = [&]<int P>() {

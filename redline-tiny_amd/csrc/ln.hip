@@ -1,0 +1,244 @@
+// Fused residual add + LayerNorm / RMSNorm + modulate, producing the next GEMM's A operand.
+//
+// Replaces the fused artifact of kernels/glue/ln_design.py:38-118 (microkernels ln_par / ln_p1 / ln_fin / ln_p2,
+// kernels/glue/ln_mod.cc:92-204) that run_ln.ln_run drives (redline/run_ln.py:43-57), and its RMSNorm copies
+// (kernels/vlm/rms_mod.cc with a bfp16 branch, rms16_mod.cc with a bf16 branch). The NPU kernel streams each 128-row
+// tile twice, statistics first and outputs second. Here one wave owns one row and keeps its D values in registers,
+// so x and the branch are read once. The kernel is HBM-bound: per value it reads 2 bytes of x and 2 (bf16) or 9/8
+// (packed) bytes of branch, and writes 2 bytes of x', 9/8 bytes of packed A and/or 2 bytes of bf16 A.
+//
+// Lane l of a row's wave owns the 8-value blocks l, l + 64, l + 128, ... of the row, so every load and store is a
+// coalesced 16-byte access and a wave covers 1 KB of the row per instruction. The packed output is assembled in LDS
+// in output order and written with 16-byte stores. In rowblock order the workgroup's 4 rows are one contiguous span.
+// In A-layout order the workgroup takes 16 rows, one 16-row band (sbr) of the 128-row A tiles, which is a contiguous
+// 128-block (1152-byte) span per 64-column K tile.
+#include <math.h>
+
+#include "rlbfp.h"
+#include "rlbfp_device.h"
+#include "rlbfp_host.h"
+
+namespace rl {
+
+constexpr int kLnThreads = 256;  // 4 waves
+constexpr int kLnMaxNB = 16;     // blocks per lane: D <= 64 lanes * 16 blocks * 8 = 8192
+
+struct LnArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const void* br;
+  int32_t br_fmt;
+  int64_t ld_br;
+  const uint16_t* params;
+  int64_t split_row;
+  int32_t norm;
+  uint16_t* x_out;
+  int64_t ld_xo;
+  uint8_t* a_packed;
+  int32_t a_order;
+  uint16_t* a_deq;
+  int64_t ld_a;
+  int64_t M;
+  int32_t D;
+  int32_t rows_wg;  // rows per workgroup: 4, or 16 for the A-layout order
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// float -> bf16 bits, round to nearest even (finite inputs)
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ void unpack8(u32x4 v, float f[8]) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xFFFF0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xFFFF0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xFFFF0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
+}
+
+__device__ __forceinline__ u32x4 pack8(const uint32_t b[8]) {
+  return u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+}
+
+// Template NB = blocks of 8 per lane (D / 512 rounded up); lanes whose block lies past the row end hold zeros and
+// skip every access.
+template <int NB>
+__global__ __launch_bounds__(kLnThreads) void ln_kernel(LnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t stage[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int D = a.D, nbr = D >> 3;
+  const int rpw = a.rows_wg >> 2;
+  const int64_t r0 = (int64_t)blockIdx.x * a.rows_wg;
+  const bool a_lay = a.a_order == RL_ORDER_A_LAYOUT;
+
+  for (int i = 0; i < rpw; i++) {
+    const int lr = wave * rpw + i;  // row within the workgroup
+    const int64_t r = r0 + lr;
+    if (r >= a.M) break;
+    const uint16_t* prm = a.params + (r < a.split_row ? 2 * (int64_t)D : 0);  // [g | sc] row
+
+    // x' = bf16(x + g * branch), kept as float; sum for the mean
+    float v[NB][8];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int cb = lane + 64 * j;
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[j][e] = 0.f;
+      if (cb < nbr) {
+        float xf[8], gf[8], bf[8];
+        unpack8(*reinterpret_cast<const u32x4*>(a.x + r * a.ldx + cb * 8), xf);
+        unpack8(*reinterpret_cast<const u32x4*>(prm + cb * 8), gf);
+        if (!a.br) {
+#pragma unroll
+          for (int e = 0; e < 8; e++) bf[e] = 0.f;
+        } else if (a.br_fmt == RL_BRANCH_BF16) {
+          unpack8(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.br) + r * a.ld_br + cb * 8), bf);
+        } else {
+          const int64_t blk = r * nbr + cb;
+          const Window w = load_window_safe(static_cast<const uint8_t*>(a.br), blk, a.M * nbr);
+          const uint32_t o = (uint32_t)(blk & 3);  // (9 * blk) % 4
+          const uint32_t lo = __builtin_amdgcn_alignbyte(w.w1, w.w0, o);
+          const uint32_t hi = __builtin_amdgcn_alignbyte(w.w2, w.w1, o);
+          const int sh = (int)(lo & 0xFFu) - 133;
+          const int32_t q[8] = {(int8_t)(lo >> 8), (int8_t)(lo >> 16), (int8_t)(lo >> 24), (int8_t)hi,
+                                (int8_t)(hi >> 8), (int8_t)(hi >> 16), (int8_t)(hi >> 24), (int8_t)(w.w2 >> (8 * o))};
+#pragma unroll
+          for (int e = 0; e < 8; e++) bf[e] = __builtin_amdgcn_ldexpf((float)q[e], sh);  // exact, as from_bfp16
+        }
+        uint32_t xb[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          xb[e] = bf16_rne(fmaf(gf[e], bf[e], xf[e]));  // g * branch is exact in fp32: one rounding, then RNE
+          v[j][e] = __uint_as_float(xb[e] << 16);
+          s += v[j][e];
+        }
+        if (a.x_out) *reinterpret_cast<u32x4*>(a.x_out + r * a.ld_xo + cb * 8) = pack8(xb);
+      }
+    }
+    s = wave_sum(s);
+    const float mean = a.norm == RL_NORM_LAYER ? s / (float)D : 0.f;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      if (lane + 64 * j < nbr) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float d = v[j][e] - mean;
+          ss = fmaf(d, d, ss);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    const float rstd = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+
+    // y = (x' - mean) * rstd * sc -> bfp16
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int cb = lane + 64 * j;
+      if (cb < nbr) {
+        float sf[8];
+        unpack8(*reinterpret_cast<const u32x4*>(prm + D + cb * 8), sf);
+        uint32_t u[8], b[8];
+        int32_t q[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) u[e] = __float_as_uint((v[j][e] - mean) * rstd * sf[e]);
+        const uint32_t E = encode_block(u, q, b);
+        if (a.a_deq) *reinterpret_cast<u32x4*>(a.a_deq + r * a.ld_a + cb * 8) = pack8(b);
+        if (a.a_packed) {
+          const int pos = a_lay ? (cb >> 3) * 128 + (cb & 7) * 16 + (lr >> 3) * 8 + (lr & 7) : lr * nbr + cb;
+          uint8_t* p = stage + pos * kBlockBytes;
+          p[0] = (uint8_t)E;
+#pragma unroll
+          for (int e = 0; e < 8; e++) p[1 + e] = (uint8_t)(int8_t)q[e];
+        }
+      }
+    }
+  }
+
+  if (!a.a_packed) return;
+  __syncthreads();
+  if (a_lay) {
+    // rows r0 .. r0 + 15 = band sbr of A tile mt: for K tile kt, 128 blocks at block ((mt * KT + kt) * 8 + sbr) * 128
+    const int KT = D >> 6;
+    const int64_t mt = r0 >> 7, sbr = (r0 >> 4) & 7;
+    const int chunks = KT * 72;  // 1152 bytes = 72 x 16 per K tile
+    for (int c = threadIdx.x; c < chunks; c += kLnThreads) {
+      const int kt = c / 72, w = c - kt * 72;
+      uint8_t* dst = a.a_packed + (((mt * KT + kt) * 8 + sbr) * 128) * kBlockBytes + 16 * w;
+      *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(stage + kt * 1152 + 16 * w);
+    }
+  } else {
+    // rows r0 .. r0 + nrows - 1 are one span; r0 * nbr * 9 is a multiple of 16 (r0 % 4 == 0, nbr % 8 == 0)
+    const int64_t nrows = min((int64_t)a.rows_wg, a.M - r0);
+    const int bytes = (int)(nrows * nbr * kBlockBytes);
+    uint8_t* dst = a.a_packed + r0 * nbr * kBlockBytes;
+    const int full = bytes / 16;
+    for (int c = threadIdx.x; c < full; c += kLnThreads)
+      *reinterpret_cast<u32x4*>(dst + 16 * c) = *reinterpret_cast<const u32x4*>(stage + 16 * c);
+    for (int c = full * 16 + threadIdx.x; c < bytes; c += kLnThreads) dst[c] = stage[c];
+  }
+}
+
+template <int NB>
+static int launch_nb(const LnArgs& a, hipStream_t st) {
+  const int64_t lds = a.a_packed ? (int64_t)a.rows_wg * (a.D / 8) * kBlockBytes : 0;
+  if (lds > 65536) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ln_kernel<NB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(RL_ERR_DEVICE, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  }
+  const dim3 grid((unsigned)((a.M + a.rows_wg - 1) / a.rows_wg));
+  hipLaunchKernelGGL(ln_kernel<NB>, grid, dim3(kLnThreads), (unsigned)lds, st, a);
+  return launch_status("rl_ln_modulate");
+}
+
+template <int NB>
+static int launch_upto(int nb, const LnArgs& a, hipStream_t st) {
+  if constexpr (NB > kLnMaxNB) {
+    return fail(RL_ERR_SHAPE, "D %d too large", a.D);
+  } else {
+    if (nb <= NB) return launch_nb<NB>(a, st);
+    return launch_upto<NB + 1>(nb, a, st);
+  }
+}
+
+}  // namespace rl
+
+extern "C" int rl_ln_modulate(const uint16_t* x, int64_t ldx, const void* branch, int32_t br_fmt, int64_t ld_br,
+                              const uint16_t* params, int64_t split_row, int32_t norm, uint16_t* x_out, int64_t ld_xo,
+                              uint8_t* a_packed, int32_t a_order, uint16_t* a_deq, int64_t ld_a, int64_t M, int64_t D,
+                              void* stream) {
+  using namespace rl;
+  // the leading dimension of an absent operand is not used
+  if (!branch) ld_br = D;
+  if (!x_out) ld_xo = D;
+  if (!a_deq) ld_a = D;
+  int s = rl_validate_ln(ldx, br_fmt, ld_br, norm, ld_xo, a_order, ld_a, split_row, M, D);
+  if (s) return s;
+  if (!x || !params) return fail(RL_ERR_NULL, "x or params is NULL");
+  if (!x_out && !a_packed && !a_deq) return fail(RL_ERR_NULL, "every output is NULL");
+  if (((uintptr_t)x | (uintptr_t)params | (uintptr_t)x_out | (uintptr_t)a_deq | (uintptr_t)a_packed) % 16)
+    return fail(RL_ERR_ALIGN, "x, params and the outputs must be 16-byte aligned");
+  if (branch && (uintptr_t)branch % (br_fmt == RL_BRANCH_BF16 ? 16 : 4))
+    return fail(RL_ERR_ALIGN, "branch must be 16-byte (bf16) or 4-byte (packed) aligned");
+  if ((s = check_device())) return s;
+  LnArgs a;
+  a.x = x; a.ldx = ldx;
+  a.br = branch; a.br_fmt = br_fmt; a.ld_br = ld_br;
+  a.params = params; a.split_row = split_row; a.norm = norm;
+  a.x_out = x_out; a.ld_xo = ld_xo;
+  a.a_packed = a_packed; a.a_order = a_order;
+  a.a_deq = a_deq; a.ld_a = ld_a;
+  a.M = M; a.D = (int32_t)D;
+  a.rows_wg = (a_packed && a_order == RL_ORDER_A_LAYOUT) ? 16 : 4;
+  const int nb = (int)((D / 8 + 63) / 64);
+  return launch_upto<1>(nb, a, static_cast<hipStream_t>(stream));
+}

@@ -73,25 +73,9 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const void* __restr
       const u32x4 a = p[0], b = p[1];
       u[0] = a.x; u[1] = a.y; u[2] = a.z; u[3] = a.w; u[4] = b.x; u[5] = b.y; u[6] = b.z; u[7] = b.w;
     }
-    const uint32_t E = block_exp(u);
     int32_t q[8];
     uint32_t b[8];
-    if (E >= 7u && E <= 254u) {
-      // powers of two scale exactly and v_rndne rounds half to even, so this equals the integer encoder; for these
-      // exponents every scaled value and every decoded value is a normal float
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float qf = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(__uint_as_float(u[i]), 133 - (int)E)), 127.0f);
-        q[i] = (int32_t)qf;
-        b[i] = __float_as_uint(__builtin_amdgcn_ldexpf(qf, (int)E - 133) + 0.0f) >> 16;  // exact in bf16; -0 -> +0
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        q[i] = encode_elem(u[i], E);
-        b[i] = decode_bf16_bits(q[i], E);
-      }
-    }
+    const uint32_t E = encode_block(u, q, b);
     if (packed) {
       uint8_t* s = stage + threadIdx.x * kBlockBytes;
       s[0] = (uint8_t)E;

@@ -143,6 +143,29 @@ __device__ __forceinline__ u32x4 quantize_bf16x8(u32x4 v, uint32_t* E_out = null
   return r;
 }
 
+// Encode 8 float32 bit patterns (finite) to one block: returns E, writes q and the decoded values' bf16 bits.
+// For block exponents 7..254 the float path is used: powers of two scale exactly and v_rndne rounds half to even, so
+// it equals the integer encoder (scaled values too small to be normal round to 0 either way), and every decoded
+// value is a normal float. Other exponents take the integer encoder.
+__device__ __forceinline__ uint32_t encode_block(const uint32_t u[8], int32_t q[8], uint32_t b[8]) {
+  const uint32_t E = block_exp(u);
+  if (E >= 7u && E <= 254u) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float qf = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(__uint_as_float(u[i]), 133 - (int)E)), 127.0f);
+      q[i] = (int32_t)qf;
+      b[i] = __float_as_uint(__builtin_amdgcn_ldexpf(qf, (int)E - 133) + 0.0f) >> 16;  // exact in bf16; -0 -> +0
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      q[i] = encode_elem(u[i], E);
+      b[i] = decode_bf16_bits(q[i], E);
+    }
+  }
+  return E;
+}
+
 // ---- XCD-aware workgroup order -----------------------------------------------------------------------------------
 // Workgroups are dispatched round robin over the 8 XCDs (pid % 8). Map them so that each XCD works on a contiguous
 // range of logical tiles, which then share operands in that XCD's L2.

@@ -18,6 +18,8 @@ RL_A_BF16, RL_A_BF16_QUANTIZE, RL_A_PACKED_ROWBLOCK, RL_A_PACKED_A_LAYOUT = 0, 1
 RL_ACT_NONE, RL_ACT_GELU_TANH, RL_ACT_SWIGLU = 0, 1, 2
 RL_GEMV_SILU = 3
 RL_EP_QUANTIZE_OUT = 1
+RL_NORM_LAYER, RL_NORM_RMS = 0, 1
+RL_BRANCH_BF16, RL_BRANCH_PACKED = 0, 1
 RL_MAX_GROUP = 16
 
 _ERRNAMES = {1: "RL_ERR_NULL", 2: "RL_ERR_SHAPE", 3: "RL_ERR_ARG", 4: "RL_ERR_ALIGN", 5: "RL_ERR_DEVICE",
@@ -52,9 +54,12 @@ SIGNATURES = {
     "rl_bfp16_gemm": (ctypes.c_int, [_P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue), _P]),
     "rl_bfp16_gemm_grouped": (ctypes.c_int, [ctypes.POINTER(GemmDesc), _I32, _I32, _P]),
     "rl_bfp16_gemv": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I32, _P]),
+    "rl_ln_modulate": (ctypes.c_int, [_P, _I64, _P, _I32, _I64, _P, _I64, _I32, _P, _I64, _P, _I32, _P, _I64, _I64,
+                                      _I64, _P]),
     "rl_validate_quantize": (ctypes.c_int, [_I32, _I64, _I64, _I64, _I32]),
     "rl_validate_gemm": (ctypes.c_int, [_I32, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue)]),
     "rl_validate_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I32]),
+    "rl_validate_ln": (ctypes.c_int, [_I64, _I32, _I64, _I32, _I64, _I32, _I64, _I64, _I64, _I64]),
     "rl_packed_bytes": (ctypes.c_int64, [_I64, _I64]),
     "rl_last_error": (ctypes.c_char_p, []),
     "rl_version": (ctypes.c_char_p, []),

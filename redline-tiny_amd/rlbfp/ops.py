@@ -1,5 +1,5 @@
 """Tensor-level entry points over librlbfp: quantize / dequantize, the packed-weight GEMM with its fused epilogues,
-grouped GEMMs and the GEMV. Inputs are torch tensors on a ROCm device (gfx950); outputs are allocated here with
+grouped GEMMs, the GEMV, and the residual + LayerNorm/RMSNorm + modulate pass that produces a GEMM's A. Inputs are torch tensors on a ROCm device (gfx950); outputs are allocated here with
 torch's caching allocator (or passed in) and the work is enqueued on torch's current stream.
 
 Packed streams are uint8 tensors of 9 bytes per 8 values. Packed weights are the bytes redline/pack_weights.py writes:
@@ -212,3 +212,49 @@ def gemv(x, b_packed, N, act="silu", out=None):
     L.check(L.lib().rl_bfp16_gemv(_ptr(x), x.stride(0), _ptr(b_packed), _ptr(out), out.stride(0), M, N, K, code,
                                   _stream(x)))
     return out
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# residual add + LayerNorm / RMSNorm + modulate -> A
+# ---------------------------------------------------------------------------------------------------------------
+
+_NORMS = {"layer": L.RL_NORM_LAYER, "rms": L.RL_NORM_RMS}
+_A_ORDERS = {"rowblock": L.RL_ORDER_ROWBLOCK, "a_layout": L.RL_ORDER_A_LAYOUT}
+
+
+def ln_modulate(x, params, branch=None, split_row=0, norm="layer", x_out=None, packed=True, a_order="rowblock",
+                deq=True):
+    """x' = bf16(x + g * branch) and y = norm(x') * sc quantized to bfp16, per row of x (M, D) bf16.
+
+    params: (2, 2D) bf16, row p = [g (D) | sc (D)]; rows < split_row use row 1, the rest row 0. branch: (M, D) bf16,
+    or a uint8 stream of bfp16 blocks in row-block order (9 * M * D / 8 bytes), or None. norm: "layer" (mean and
+    variance, eps 1e-6) or "rms". x_out: where x' goes (may be x itself; None allocates). Returns (x', A packed bytes
+    in a_order or None, A as bf16 or None); see rl_ln_modulate in include/rlbfp.h."""
+    _dev(x, "x")
+    _dev(params, "params")
+    if x.dim() != 2 or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("x must be a 2-D bfloat16 tensor with unit column stride")
+    M, D = x.shape
+    if params.dtype != torch.bfloat16 or params.numel() != 4 * D or not params.is_contiguous():
+        raise ValueError(f"params must be a contiguous bfloat16 (2, {2 * D}) tensor")
+    br_fmt, ld_br = L.RL_BRANCH_BF16, D
+    if branch is not None:
+        _dev(branch, "branch")
+        if branch.dtype == torch.uint8:
+            if branch.numel() != packed_bytes(M, D):
+                raise ValueError(f"a packed branch must hold {packed_bytes(M, D)} bytes")
+            br_fmt = L.RL_BRANCH_PACKED
+        elif branch.dtype == torch.bfloat16 and branch.shape == (M, D) and branch.stride(1) == 1:
+            ld_br = branch.stride(0)
+        else:
+            raise ValueError("branch must be (M, D) bfloat16 or a uint8 bfp16 stream")
+    if x_out is None:
+        x_out = torch.empty_like(x)
+    elif x_out.dtype != torch.bfloat16 or x_out.shape != (M, D) or x_out.stride(1) != 1:
+        raise ValueError("x_out must be (M, D) bfloat16 with unit column stride")
+    a_p = torch.empty(packed_bytes(M, D), dtype=torch.uint8, device=x.device) if packed else None
+    a_d = torch.empty((M, D), dtype=torch.bfloat16, device=x.device) if deq else None
+    L.check(L.lib().rl_ln_modulate(_ptr(x), x.stride(0), _ptr(branch), br_fmt, ld_br, _ptr(params), split_row,
+                                   _NORMS[norm], _ptr(x_out), x_out.stride(0), _ptr(a_p), _A_ORDERS[a_order],
+                                   _ptr(a_d), D, M, D, _stream(x)))
+    return x_out, a_p, a_d

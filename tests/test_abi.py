@@ -98,3 +98,29 @@ def test_null_pointers_rejected_before_any_gpu_call():
     assert s == L.RL_ERR_NULL
     s = lib.rl_bfp16_gemm_grouped(None, 1, 0, None)
     assert s == L.RL_ERR_NULL
+
+
+@pytest.mark.parametrize("args,code", [
+    ((3072, L.RL_BRANCH_BF16, 3072, L.RL_NORM_LAYER, 3072, L.RL_ORDER_ROWBLOCK, 3072, 0, 4352, 3072), L.RL_OK),
+    ((4096, L.RL_BRANCH_PACKED, 0, L.RL_NORM_RMS, 4096, L.RL_ORDER_A_LAYOUT, 4096, 0, 512, 4096), L.RL_OK),
+    ((3072, L.RL_BRANCH_BF16, 3072, L.RL_NORM_LAYER, 3072, L.RL_ORDER_A_LAYOUT, 3072, 0, 100, 3072), L.RL_ERR_SHAPE),
+    ((96, L.RL_BRANCH_BF16, 96, L.RL_NORM_LAYER, 96, L.RL_ORDER_ROWBLOCK, 96, 0, 4, 96), L.RL_ERR_SHAPE),
+    ((16384, L.RL_BRANCH_BF16, 16384, L.RL_NORM_LAYER, 16384, L.RL_ORDER_ROWBLOCK, 16384, 0, 4, 16384),
+     L.RL_ERR_SHAPE),
+    ((3072, 7, 3072, L.RL_NORM_LAYER, 3072, L.RL_ORDER_ROWBLOCK, 3072, 0, 8, 3072), L.RL_ERR_ARG),
+    ((3072, L.RL_BRANCH_BF16, 3072, 5, 3072, L.RL_ORDER_ROWBLOCK, 3072, 0, 8, 3072), L.RL_ERR_ARG),
+    ((3072, L.RL_BRANCH_BF16, 3072, L.RL_NORM_LAYER, 3072, L.RL_ORDER_C_ATB, 3072, 0, 512, 3072), L.RL_ERR_ARG),
+    ((3072, L.RL_BRANCH_BF16, 3072, L.RL_NORM_LAYER, 3072, L.RL_ORDER_ROWBLOCK, 3072, -1, 8, 3072), L.RL_ERR_ARG),
+    ((3070, L.RL_BRANCH_BF16, 3072, L.RL_NORM_LAYER, 3072, L.RL_ORDER_ROWBLOCK, 3072, 0, 8, 3072), L.RL_ERR_ALIGN),
+    ((3072, L.RL_BRANCH_BF16, 3076, L.RL_NORM_LAYER, 3072, L.RL_ORDER_ROWBLOCK, 3072, 0, 8, 3072), L.RL_ERR_ALIGN),
+])
+def test_validate_ln(args, code):
+    assert L.lib().rl_validate_ln(*args) == code
+
+
+def test_ln_null_pointers_rejected_before_any_gpu_call():
+    lib = L.lib()
+    s = lib.rl_ln_modulate(None, 64, None, 0, 64, None, 0, 0, None, 64, None, 0, None, 64, 4, 64, None)
+    assert s == L.RL_ERR_NULL
+    s = lib.rl_ln_modulate(16, 64, None, 0, 64, 16, 0, 0, None, 0, None, 0, None, 0, 4, 64, None)
+    assert s == L.RL_ERR_NULL  # every output NULL

@@ -12,7 +12,8 @@ library runs that call as two launches of the same kernel (rows 0..4095 in 256-r
 CUs, then the last 256 rows in 128-row tiles), timed together. Kernel times are medians of HIP-event intervals on the
 launch stream.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
-rotating weight copies so that the 256 MB MALL cannot hold them, and the CPU baseline (the oracle's numpy restatement
+rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
+produces the up GEMM's A (4352 x 3072) in GB/s against HBM; and the CPU baseline (the oracle's numpy restatement
 of the reference CPU path on a row sample of the same workload).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--copy-probe MB] [--sustain SECONDS]
@@ -193,7 +194,68 @@ def gpu_bench(steps, warmup):
         "wall_s": wall, "ms_step": ms_step, "ms_step_eager": ms_step_eager,
         "ms_q": ms_q, "ms_up": ms_up, "ms_down": ms_down, "us_gemv": us_gemv,
         "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
+        "ln": ln_bench(dev),
     }
+
+
+def ln_bench(dev, sets=4, per_graph=40, reps=4):
+    """The residual + LayerNorm + modulate pass that produces the up GEMM's A (M x hidden = 4352 x 3072), in two
+    configurations, each as HIP-graph replays of `per_graph` launches rotating over `sets` input sets (4 x 53 MB of
+    inputs plus the outputs exceed the 256 MB MALL):
+      native:  bf16 x, bf16 branch (a GEMM output) -> x' bf16 and A as bf16 (the next GEMM's operand): 8 B per value
+      packed:  bf16 x, bfp16 branch (row blocks) -> x' bf16 and A as bfp16 (the reference's formats): 6.25 B per value
+    Algorithmic bytes are those reads and writes once each; the 2 x 2D bf16 parameters are not counted."""
+    import ctypes
+
+    import torch
+
+    from rlbfp import _lib as L
+    from rlbfp import ops
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    xs = [torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for _ in range(sets)]
+    brs = [torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16) for _ in range(sets)]
+    brp = [ops.quantize(b)[0] for b in brs]
+    params = torch.cat([torch.tanh(torch.randn((2, K), generator=g, device=dev)),
+                        1 + 0.3 * torch.randn((2, K), generator=g, device=dev)], 1).to(torch.bfloat16).contiguous()
+    xo = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    a_d = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    a_p = torch.empty(M * K // 8 * 9, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+    def call(i, packed):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        br, fmt = (brp[i % sets], L.RL_BRANCH_PACKED) if packed else (brs[i % sets], L.RL_BRANCH_BF16)
+        L.check(L.lib().rl_ln_modulate(P(xs[i % sets]), K, P(br), fmt, K, P(params), 0, L.RL_NORM_LAYER, P(xo), K,
+                                       P(a_p if packed else None), L.RL_ORDER_ROWBLOCK, P(None if packed else a_d),
+                                       K, M, K, st))
+
+    out = {"shape": [M, K], "norm": "layer", "sets": sets}
+    for name, packed, bpv in (("native", False, 8.0), ("packed", True, 2 + 9 / 8 + 2 + 9 / 8)):
+        for i in range(2 * sets):
+            call(i, packed)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(per_graph):
+                    call(i, packed)
+        torch.cuda.current_stream().wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+        gbps = M * K * bpv / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "bytes": int(M * K * bpv), "gbps": round(gbps, 1),
+                     "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4)}
+    return out
 
 
 def cpu_baseline(host, p_up, p_down, rows=M, runs=3):
@@ -379,6 +441,7 @@ def main():
         "gemv": {"shape": [1, GEMV_K, GEMV_N], "us": round(r["us_gemv"], 2), "gbps": round(r["gemv_gbps"], 1),
                  "frac_hbm": round(r["gemv_gbps"] / PEAK_HBM_GBPS, 4), "bytes": int(r["gemv_bytes"]),
                  "copies": 6},
+        "ln_modulate": r["ln"],
     }
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(r["host"], r["p_up"], r["p_down"])
     print(json.dumps(line), flush=True)

@@ -67,9 +67,14 @@ __device__ __forceinline__ u32x4 pack8(const uint32_t b[8]) {
 }
 
 // Template NB = blocks of 8 per lane (D / 512 rounded up); lanes whose block lies past the row end hold zeros and
-// skip every access.
+// skip every access. The register budget per NB is the smallest that compiles without spills; for D = 3072 (NB 6)
+// it allows 5 waves per SIMD, so a launch of one wave per row for M = 4352 rows is resident in one round (at 4 waves
+// per SIMD a second, partial round would follow).
 template <int NB>
-__global__ __launch_bounds__(kLnThreads) void ln_kernel(LnArgs a) {
+constexpr int ln_waves_per_simd() { return NB <= 5 ? 6 : NB <= 7 ? 5 : NB <= 13 ? 4 : 3; }
+
+template <int NB>
+__global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel(LnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t stage[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -84,14 +89,14 @@ __global__ __launch_bounds__(kLnThreads) void ln_kernel(LnArgs a) {
     if (r >= a.M) break;
     const uint16_t* prm = a.params + (r < a.split_row ? 2 * (int64_t)D : 0);  // [g | sc] row
 
-    // x' = bf16(x + g * branch), kept as float; sum for the mean
-    float v[NB][8];
+    // x' = bf16(x + g * branch), kept as its bf16 bits (two per register: the row stays resident at 4 registers
+    // per block); sum for the mean
+    u32x4 v[NB];
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int cb = lane + 64 * j;
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[j][e] = 0.f;
+      v[j] = u32x4{0u, 0u, 0u, 0u};
       if (cb < nbr) {
         float xf[8], gf[8], bf[8];
         unpack8(*reinterpret_cast<const u32x4*>(a.x + r * a.ldx + cb * 8), xf);
@@ -117,10 +122,10 @@ __global__ __launch_bounds__(kLnThreads) void ln_kernel(LnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           xb[e] = bf16_rne(fmaf(gf[e], bf[e], xf[e]));  // g * branch is exact in fp32: one rounding, then RNE
-          v[j][e] = __uint_as_float(xb[e] << 16);
-          s += v[j][e];
+          s += __uint_as_float(xb[e] << 16);
         }
-        if (a.x_out) *reinterpret_cast<u32x4*>(a.x_out + r * a.ld_xo + cb * 8) = pack8(xb);
+        v[j] = pack8(xb);
+        if (a.x_out) *reinterpret_cast<u32x4*>(a.x_out + r * a.ld_xo + cb * 8) = v[j];
       }
     }
     s = wave_sum(s);
@@ -129,9 +134,11 @@ __global__ __launch_bounds__(kLnThreads) void ln_kernel(LnArgs a) {
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       if (lane + 64 * j < nbr) {
+        float xf[8];
+        unpack8(v[j], xf);
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-          const float d = v[j][e] - mean;
+          const float d = xf[e] - mean;
           ss = fmaf(d, d, ss);
         }
       }
@@ -144,12 +151,13 @@ __global__ __launch_bounds__(kLnThreads) void ln_kernel(LnArgs a) {
     for (int j = 0; j < NB; j++) {
       const int cb = lane + 64 * j;
       if (cb < nbr) {
-        float sf[8];
+        float sf[8], xf[8];
         unpack8(*reinterpret_cast<const u32x4*>(prm + D + cb * 8), sf);
+        unpack8(v[j], xf);
         uint32_t u[8], b[8];
         int32_t q[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) u[e] = __float_as_uint((v[j][e] - mean) * rstd * sf[e]);
+        for (int e = 0; e < 8; e++) u[e] = __float_as_uint((xf[e] - mean) * rstd * sf[e]);
         const uint32_t E = encode_block(u, q, b);
         if (a.a_deq) *reinterpret_cast<u32x4*>(a.a_deq + r * a.ld_a + cb * 8) = pack8(b);
         if (a.a_packed) {

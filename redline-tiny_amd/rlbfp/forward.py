@@ -1,7 +1,7 @@
 """The DiT GEMM call surface of redline/forward.py, on the HIP path.
 
 Names, arguments and meaning follow the reference: ``GEMMS`` (artifact name per (op, M)), ``GEMM_KN``, ``v9``,
-``NPU.run(op, art, args)`` / ``NPU.sync()`` / ``NPU.report()``, ``Weights`` (the packed ``bNN_*.bin`` files plus
+``NPU.run(op, art, args)`` / ``NPU.sync()`` / ``NPU.report()`` (GEMMs and the "ln_mod" pass), ``Weights`` (the packed ``bNN_*.bin`` files plus
 ``manifest.json`` that redline/pack_weights.py writes) and ``gemm(npu, w, op, M, a, c, block=None)``
 (redline/forward.py:33-44, :82-84, :87-172, :175-197).
 
@@ -24,12 +24,13 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from . import ops
+from . import ops, run_ln
 
 N_BLOCKS, HID, FF = 32, 4096, 12288
 M_S1 = 8704
 
 # artifact names per (op, M) as in redline/forward.py:33-42; here they select the epilogue of the HIP GEMM
+LN_ART = {4096: "glue-ln-m4096-s0", M_S1: "glue-ln-m8704-s33"}  # redline/forward.py:205
 GEMMS = {
     ("qkv", 4096): "atb3d2-qkv", ("qkv", M_S1): "atb3d2-s1qkv",
     ("o", 4096): "atb3d2-4096", ("o", M_S1): "atb3d2-s1o",
@@ -75,12 +76,17 @@ class NPU:
         self.pending = []
 
     def run(self, op, art, args):
-        """args = [A, B, C] (or [A, W_up, H] for up_swiglu); see the module docstring for the accepted forms."""
-        a, b, c = args
+        """args = [A, B, C] (or [A, W_up, H] for up_swiglu), see the module docstring for the accepted forms; or
+        [X, BR, P, XO, AO] for the fused residual + LayerNorm + modulate artifacts ("ln_mod", glue-ln-m{M}-s{S}, and
+        the RMSNorm copies), run by run_ln.ln_fused."""
         t = time.perf_counter()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        self._gemm(op, art, a, b, c)
+        if len(args) == 5:
+            run_ln.ln_fused(art, *args)
+        else:
+            a, b, c = args
+            self._gemm(op, art, a, b, c)
         e1.record()
         self.pending.append((op, e0, e1, list(args)))
         self.t_wall[op] += time.perf_counter() - t

@@ -150,10 +150,32 @@ int rl_ln_modulate(const uint16_t *x, int64_t ldx, const void *branch, int32_t b
                    uint8_t *a_packed, int32_t a_order, uint16_t *a_deq, int64_t ld_a, int64_t M, int64_t D,
                    void *stream);
 
+/* ---- QKV post: the QKV GEMM output -> attention Q / K / V --------------------------------------------------------
+ * C (M, 3 * heads * 128) bf16 row major (ldc): per token row the q, k and v columns of `heads` heads of 128 dims.
+ * Per head and token row, in fp32:
+ *   Q = rope(rms(q) * wq), K = rope(rms(k) * wk), V = v,
+ * with rms(x) = x / sqrt(mean(x^2) + 1e-6) over the head's 128 dims, and rope the rotation of each dim pair
+ * (2i, 2i+1) by (cos, sin)[row][i] (run_glue.rms_rope / rope, redline/run_glue.py:27-37). Q and K are quantized to
+ * bfp16 in blocks of 8 dims, V in blocks of 8 tokens of one dim.
+ * cos, sin: (M, 64) bf16 each, row major; wq (the attention score scale log2(e)/sqrt(128) folded in, as
+ * redline/run_qkv.py:27 does) and wk: 128 bf16 each.
+ * Outputs (each may be NULL, not all):
+ *   q_tiles  (heads, M/64, 9216 bytes): per head and 64-token tile, to_bfp16(a_layout(Q tile, 64, 128));
+ *   kv_tiles (heads, M/64, 2, 9216 bytes): to_bfp16(b_layout(K tile^T, 128, 64)), then to_bfp16(b_layout(V tile, 64,
+ *            128)) (the attention kernel's formats, kernels/glue/qkv_post.cc:1-16);
+ *   q, k, v  (heads, M, 128) bf16 each: the same quantized values, head major.
+ * M % 64 == 0, heads >= 1.
+ * Replaces the QKV-post artifact (kernels/glue/qkv_design.py:40-118 with qkv_post.cc:134-177) run by
+ * run_qkv.qkv32_npu (redline/run_qkv.py:67-82). */
+int rl_qkv_post(const uint16_t *C, int64_t ldc, int64_t M, int32_t heads, const uint16_t *cos, const uint16_t *sin,
+                const uint16_t *wq, const uint16_t *wk, uint8_t *q_tiles, uint8_t *kv_tiles, uint16_t *q, uint16_t *k,
+                uint16_t *v, void *stream);
+
 /* ---- host-only helpers (no GPU needed) ---------------------------------------------------------------------------- */
 /* Shape/argument checks the entry points run before launching, callable on a machine without a GPU. */
 int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int64_t ld_xo, int32_t a_order,
                    int64_t ld_a, int64_t split_row, int64_t M, int64_t D);
+int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads);
 int rl_validate_quantize(int32_t x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int32_t order);
 int rl_validate_gemm(int32_t a_fmt, int64_t lda, int64_t ldc, int64_t M, int64_t N, int64_t K, const rl_epilogue *ep);
 int rl_validate_gemv(int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t act);

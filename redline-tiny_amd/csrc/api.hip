@@ -160,4 +160,15 @@ int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int
   return rl::ok();
 }
 
+int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads) {
+  using rl::fail;
+  if (heads < 1 || heads > 1024) return fail(RL_ERR_SHAPE, "heads %d: need 1..1024", heads);
+  if (M < 64 || M % 64 || M > (1 << 30))
+    return fail(RL_ERR_SHAPE, "M %lld: need a positive multiple of 64", (long long)M);
+  if (M / 64 * heads > ((int64_t)1 << 31) - 1) return fail(RL_ERR_SHAPE, "more than 2^31 tiles");
+  if (ldc < 3 * 128 * (int64_t)heads || ldc % 8)
+    return fail(RL_ERR_ALIGN, "ldc %lld: need >= 3 * 128 * heads and a multiple of 8", (long long)ldc);
+  return rl::ok();
+}
+
 }  // extern "C"

@@ -77,3 +77,36 @@ def c_unlayout_atb_values(s, M, N):
     out = torch.empty((M * N // 8, 8), dtype=s.dtype, device=s.device)
     out[c_atb_block_index(M, N, s.device)] = s.reshape(-1, 8)
     return out.reshape(M, N)
+
+
+def a_block_index(R, C, m, k, device="cuda"):
+    """Stream block index, in a_layout(., m, k) (redline/npu_layouts.py:18-22), of each row-major block (r, c / 8):
+    (m, k) tiles row major, then 16-row bands, 8-column blocks, the two 8-row halves, row."""
+    r = torch.arange(R, device=device, dtype=torch.int64)[:, None]
+    cb = torch.arange(C // 8, device=device, dtype=torch.int64)[None, :]
+    c = cb * 8
+    t = (r // m) * (C // k) + c // k
+    return ((((t * (m // 16) + (r % m) // 16) * (k // 8) + (c % k) // 8) * 2 + (r % 16) // 8) * 8 + r % 8).reshape(-1)
+
+
+def b_block_index(K, N, k, n, device="cuda"):
+    """Stream block index, in b_layout(., k, n) (redline/npu_layouts.py:11-15), of each block (k-block kb, column c)
+    of a (K, N) matrix, blocks = 8 consecutive rows of one column; indexed kb * N + c: (k, n) tiles column-tile major,
+    then 16-column bands, 8-row blocks, the two 8-column halves, column."""
+    kb = torch.arange(K // 8, device=device, dtype=torch.int64)[:, None]
+    c = torch.arange(N, device=device, dtype=torch.int64)[None, :]
+    r = kb * 8
+    t = (c // n) * (K // k) + r // k
+    return ((((t * (n // 16) + (c % n) // 16) * (k // 8) + (r % k) // 8) * 2 + (c % 16) // 8) * 8 + c % 8).reshape(-1)
+
+
+def a_unlayout(raw, R, C, m, k):
+    """bfp16 bytes of a_layout(x, m, k) -> x (R, C) float32."""
+    blocks = from_bfp16(raw).reshape(-1, 8)
+    return blocks[a_block_index(R, C, m, k, raw.device)].reshape(R, C)
+
+
+def b_unlayout(raw, K, N, k, n):
+    """bfp16 bytes of b_layout(b, k, n) -> b (K, N) float32."""
+    blocks = from_bfp16(raw).reshape(-1, 8)[b_block_index(K, N, k, n, raw.device)]  # (K/8 * N, 8): [kb, c, e]
+    return blocks.reshape(K // 8, N, 8).permute(0, 2, 1).reshape(K, N)

@@ -1,6 +1,7 @@
 """Tensor-level entry points over librlbfp: quantize / dequantize, the packed-weight GEMM with its fused epilogues,
-grouped GEMMs, the GEMV, and the residual + LayerNorm/RMSNorm + modulate pass that produces a GEMM's A. Inputs are torch tensors on a ROCm device (gfx950); outputs are allocated here with
-torch's caching allocator (or passed in) and the work is enqueued on torch's current stream.
+grouped GEMMs, the GEMV, the residual + LayerNorm/RMSNorm + modulate pass that produces a GEMM's A, and the QKV post
+pass (per-head RMSNorm + RoPE -> attention tiles). Inputs are torch tensors on a ROCm device (gfx950); outputs are
+allocated here with torch's caching allocator (or passed in) and the work is enqueued on torch's current stream.
 
 Packed streams are uint8 tensors of 9 bytes per 8 values. Packed weights are the bytes redline/pack_weights.py writes:
 to_bfp16(b_layout(W.T, 64, 128)) of a Linear weight W (N, K).
@@ -258,3 +259,33 @@ def ln_modulate(x, params, branch=None, split_row=0, norm="layer", x_out=None, p
                                    _NORMS[norm], _ptr(x_out), x_out.stride(0), _ptr(a_p), _A_ORDERS[a_order],
                                    _ptr(a_d), D, M, D, _stream(x)))
     return x_out, a_p, a_d
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# QKV post -> attention Q / K / V
+# ---------------------------------------------------------------------------------------------------------------
+
+def qkv_post(C, cos, sin, wq, wk, heads, tiles=True, native=False):
+    """Per head of 128 dims: Q = rope(rms(q) * wq), K = rope(rms(k) * wk), V = v, quantized to bfp16 (Q, K in blocks
+    of 8 dims, V in blocks of 8 tokens). C (M, 3 * heads * 128) bf16; cos, sin (M, 64) bf16; wq, wk (128,) bf16.
+    Returns (q_tiles (heads, M/64, 9216) uint8, kv_tiles (heads, M/64, 2, 9216) uint8) if tiles, else None, None;
+    then (q, k, v) each (heads, M, 128) bf16 if native, else None x 3. See rl_qkv_post in include/rlbfp.h."""
+    for t, n in ((C, "C"), (cos, "cos"), (sin, "sin"), (wq, "wq"), (wk, "wk")):
+        _dev(t, n)
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{n} must be bfloat16")
+    M = C.shape[0]
+    if C.dim() != 2 or C.stride(1) != 1 or C.shape[1] != 3 * 128 * heads:
+        raise ValueError(f"C must be (M, {3 * 128 * heads}) with unit column stride")
+    if cos.shape != (M, 64) or sin.shape != (M, 64) or not cos.is_contiguous() or not sin.is_contiguous():
+        raise ValueError("cos and sin must be contiguous (M, 64)")
+    if wq.numel() != 128 or wk.numel() != 128 or not wq.is_contiguous() or not wk.is_contiguous():
+        raise ValueError("wq and wk must be contiguous 128-vectors")
+    T = M // 64
+    qt = torch.empty((heads, T, 9216), dtype=torch.uint8, device=C.device) if tiles else None
+    kvt = torch.empty((heads, T, 2, 9216), dtype=torch.uint8, device=C.device) if tiles else None
+    q, k, v = ((torch.empty((heads, M, 128), dtype=torch.bfloat16, device=C.device) for _ in range(3)) if native
+               else (None, None, None))
+    L.check(L.lib().rl_qkv_post(_ptr(C), C.stride(0), M, heads, _ptr(cos), _ptr(sin), _ptr(wq), _ptr(wk), _ptr(qt),
+                                _ptr(kvt), _ptr(q), _ptr(k), _ptr(v), _stream(C)))
+    return qt, kvt, q, k, v

@@ -124,3 +124,23 @@ def test_ln_null_pointers_rejected_before_any_gpu_call():
     assert s == L.RL_ERR_NULL
     s = lib.rl_ln_modulate(16, 64, None, 0, 64, 16, 0, 0, None, 0, None, 0, None, 0, 4, 64, None)
     assert s == L.RL_ERR_NULL  # every output NULL
+
+
+@pytest.mark.parametrize("args,code", [
+    ((9216, 4352, 24), L.RL_OK),
+    ((12288, 4096, 32), L.RL_OK),
+    ((9216, 4350, 24), L.RL_ERR_SHAPE),
+    ((9216, 0, 24), L.RL_ERR_SHAPE),
+    ((9216, 4352, 0), L.RL_ERR_SHAPE),
+    ((9000, 4352, 24), L.RL_ERR_ALIGN),
+    ((9220, 4352, 24), L.RL_ERR_ALIGN),
+])
+def test_validate_qkv_post(args, code):
+    assert L.lib().rl_validate_qkv_post(*args) == code
+
+
+def test_qkv_post_null_pointers_rejected_before_any_gpu_call():
+    lib = L.lib()
+    assert lib.rl_qkv_post(None, 384, 64, 1, None, None, None, None, None, None, None, None, None, None) == \
+        L.RL_ERR_NULL
+    assert lib.rl_qkv_post(16, 384, 64, 1, 16, 16, 16, 16, None, None, None, None, None, None) == L.RL_ERR_NULL

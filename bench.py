@@ -13,8 +13,8 @@ CUs, then the last 256 rows in 128-row tiles), timed together. Kernel times are 
 launch stream.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
 rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
-produces the up GEMM's A (4352 x 3072) in GB/s against HBM; and the CPU baseline (the oracle's numpy restatement
-of the reference CPU path on a row sample of the same workload).
+produces the up GEMM's A (4352 x 3072) and the QKV post pass (4352 tokens x 24 heads) in GB/s against HBM; and the
+CPU baseline (the oracle's numpy restatement of the reference CPU path on a row sample of the same workload).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--copy-probe MB] [--sustain SECONDS]
 """
@@ -195,6 +195,7 @@ def gpu_bench(steps, warmup):
         "ms_q": ms_q, "ms_up": ms_up, "ms_down": ms_down, "us_gemv": us_gemv,
         "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
         "ln": ln_bench(dev),
+        "qkv": qkv_bench(dev),
     }
 
 
@@ -232,30 +233,72 @@ def ln_bench(dev, sets=4, per_graph=40, reps=4):
 
     out = {"shape": [M, K], "norm": "layer", "sets": sets}
     for name, packed, bpv in (("native", False, 8.0), ("packed", True, 2 + 9 / 8 + 2 + 9 / 8)):
-        for i in range(2 * sets):
-            call(i, packed)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(graph, stream=side):
-                for i in range(per_graph):
-                    call(i, packed)
-        torch.cuda.current_stream().wait_stream(side)
-        graph.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+        us = graph_us(lambda i: call(i, packed), 2 * sets, per_graph, reps)
         gbps = M * K * bpv / (us * 1e-6) / 1e9
         out[name] = {"us": round(us, 2), "bytes": int(M * K * bpv), "gbps": round(gbps, 1),
                      "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4)}
     return out
+
+
+def graph_us(call, warm, per_graph, reps):
+    """Microseconds per call(i): `warm` eager calls, then `per_graph` calls captured in one HIP graph (i = 0, 1, ...)
+    and replayed `reps` times between two events."""
+    import torch
+
+    for i in range(warm):
+        call(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(per_graph):
+                call(i)
+    torch.cuda.current_stream().wait_stream(side)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def qkv_bench(dev, heads=24, sets=3, per_graph=30, reps=4):
+    """The QKV post pass on the QKV GEMM output of the benchmark's M (4352 tokens x 3 x 24 heads of 128 = hidden 3072):
+    bf16 C in, the attention Q / K / V tiles (bfp16) out; HIP-graph replays rotating over `sets` copies of C
+    (3 x 80 MB with the outputs exceed the 256 MB MALL). Algorithmic bytes: C read once (2 B per value) and the tiles
+    written once (9/8 B per value); the cos/sin rows (1.1 MB) and weights are not counted."""
+    import ctypes
+
+    import torch
+
+    from rlbfp import _lib as L
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    n = 3 * heads * 128
+    Cs = [torch.randn((M, n), generator=g, device=dev).to(torch.bfloat16) for _ in range(sets)]
+    ang = torch.rand((M, 64), generator=g, device=dev) * 6.2832
+    cos, sin = torch.cos(ang).to(torch.bfloat16), torch.sin(ang).to(torch.bfloat16)
+    wq = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(128, generator=g, device=dev)).to(torch.bfloat16)
+    qt = torch.empty((heads, M // 64, 9216), dtype=torch.uint8, device=dev)
+    kvt = torch.empty((heads, M // 64, 2, 9216), dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+    def call(i):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        L.check(L.lib().rl_qkv_post(P(Cs[i % sets]), n, M, heads, P(cos), P(sin), P(wq), P(wk), P(qt), P(kvt),
+                                    P(None), P(None), P(None), st))
+
+    us = graph_us(call, 2 * sets, per_graph, reps)
+    nbytes = M * n * (2 + 9 / 8)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"shape": [M, heads, 128], "us": round(us, 2), "bytes": int(nbytes), "gbps": round(gbps, 1),
+            "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4), "sets": sets}
 
 
 def cpu_baseline(host, p_up, p_down, rows=M, runs=3):
@@ -442,6 +485,7 @@ def main():
                  "frac_hbm": round(r["gemv_gbps"] / PEAK_HBM_GBPS, 4), "bytes": int(r["gemv_bytes"]),
                  "copies": 6},
         "ln_modulate": r["ln"],
+        "qkv_post": r["qkv"],
     }
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(r["host"], r["p_up"], r["p_down"])
     print(json.dumps(line), flush=True)

@@ -165,7 +165,7 @@ int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads) {
   if (heads < 1 || heads > 1024) return fail(RL_ERR_SHAPE, "heads %d: need 1..1024", heads);
   if (M < 64 || M % 64 || M > (1 << 30))
     return fail(RL_ERR_SHAPE, "M %lld: need a positive multiple of 64", (long long)M);
-  if (M / 64 * heads > ((int64_t)1 << 31) - 1) return fail(RL_ERR_SHAPE, "more than 2^31 tiles");
+  if (M / 64 * heads * 3 > ((int64_t)1 << 31) - 1) return fail(RL_ERR_SHAPE, "more than 2^31 tiles");
   if (ldc < 3 * 128 * (int64_t)heads || ldc % 8)
     return fail(RL_ERR_ALIGN, "ldc %lld: need >= 3 * 128 * heads and a multiple of 8", (long long)ldc);
   return rl::ok();

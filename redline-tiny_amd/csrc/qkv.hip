@@ -2,14 +2,14 @@
 //
 // Replaces the QKV-post artifact of kernels/glue/qkv_design.py:40-118 (microkernels q_post / k_post / v_post,
 // kernels/glue/qkv_post.cc:134-177) that run_qkv.qkv32_npu drives (redline/run_qkv.py:67-82). One workgroup takes
-// one head of one 64-token tile: 64 x 128 values each of q, k and v (48 KB of bf16 in), and writes the three 9216-byte
-// tiles the attention kernel reads. The pass is HBM-bound: 2 bytes read and 9/8 bytes written per value (plus 2 per
-// value for each bf16 output requested).
+// one part (q, k or v) of one head of one 64-token tile: 64 x 128 values (16 KB of bf16 in), and writes the 9216-byte
+// tile the attention kernel reads. The pass is HBM-bound: 2 bytes read and 9/8 bytes written per value (plus 2 per
+// value for each bf16 output requested). Small workgroups (9 KB of LDS) keep many tiles in flight per CU.
 //
 // Q and K: thread (token r, 8-dim block bc) holds 8 dims of one token; the 16 threads of a token (16 lanes of a wave)
 // reduce the sum of squares across their lanes. RoPE pairs (2i, 2i + 1) lie inside a block, so each thread rotates
-// its own 4 pairs. V: the tile is staged in LDS and each thread reads 8 tokens of one dim, the block V is quantized
-// in. The three tiles are assembled in LDS in output order and written with 16-byte stores.
+// its own 4 pairs. V: each thread reads the 8 tokens of one dim that a V block holds. The tile is assembled in LDS
+// in output order and written with 16-byte stores.
 #include <math.h>
 
 #include "rlbfp.h"
@@ -23,7 +23,6 @@ constexpr int kHeadDim = 128;
 constexpr int kTileTokens = 64;
 constexpr int kTileBlocks = kTileTokens * kHeadDim / 8;     // 1024
 constexpr int kTile9 = kTileBlocks * kBlockBytes;          // 9216
-constexpr int kVPitch = kHeadDim + 8;                       // bf16 per staged V row: 272 bytes
 
 struct QkvArgs {
   const uint16_t* C;
@@ -56,26 +55,19 @@ __device__ __forceinline__ void stage_block(uint8_t* stage, int pos, uint32_t E,
 }
 
 __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t stage[3][kTile9];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[kTileTokens * kVPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t stage[kTile9];
   const int tid = threadIdx.x;
-  const int h = blockIdx.x % a.heads, t = blockIdx.x / a.heads;
+  // workgroup = (part, head, tile): the three parts of one (head, tile) are neighbours in launch order
+  const int part = blockIdx.x % 3, ht = blockIdx.x / 3;
+  const int h = ht % a.heads, t = ht / a.heads;
   const int64_t row0 = (int64_t)t * kTileTokens;
   const int64_t D = (int64_t)a.heads * kHeadDim;
-  const bool tiles = a.q_tiles != nullptr || a.kv_tiles != nullptr;
+  const int64_t col0 = part * D + h * kHeadDim;
+  const bool tiles = part == 0 ? a.q_tiles != nullptr : a.kv_tiles != nullptr;
 
-  // V tile (64 tokens x 128 dims) into LDS: 1024 16-byte chunks, 4 per thread, coalesced along the row
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int c = tid + kQkvThreads * i, r = c >> 4, ch = c & 15;
-    *reinterpret_cast<u32x4*>(&vt[r * kVPitch + ch * 8]) =
-        *reinterpret_cast<const u32x4*>(a.C + (row0 + r) * a.ldc + 2 * D + h * kHeadDim + ch * 8);
-  }
-
-  // Q (part 0) and K (part 1): thread = (token rr + 16 pass, dim block bc)
-  const int bc = tid & 15, rr = tid >> 4;
-#pragma unroll
-  for (int part = 0; part < 2; part++) {
+  if (part < 2) {
+    // Q (part 0) and K (part 1): thread = (token rr + 16 pass, dim block bc)
+    const int bc = tid & 15, rr = tid >> 4;
     float wf[8];
     unpack8f(*reinterpret_cast<const u32x4*>((part ? a.wk : a.wq) + bc * 8), wf);
     uint16_t* nat = part ? a.k : a.q;
@@ -84,7 +76,7 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
       const int r = pass * 16 + rr;
       const int64_t row = row0 + r;
       float xf[8];
-      unpack8f(*reinterpret_cast<const u32x4*>(a.C + row * a.ldc + part * D + h * kHeadDim + bc * 8), xf);
+      unpack8f(*reinterpret_cast<const u32x4*>(a.C + row * a.ldc + col0 + bc * 8), xf);
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) ss = fmaf(xf[e], xf[e], ss);
@@ -111,35 +103,33 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
             u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
       // a_layout(64, 128) for Q and b_layout(K^T, 128, 64) for K order a tile's blocks the same way:
       // 16-token band, 8-dim block, 8-token half, token
-      if (tiles) stage_block(stage[part], (((r >> 4) * 16 + bc) * 2 + ((r >> 3) & 1)) * 8 + (r & 7), E, q);
+      if (tiles) stage_block(stage, (((r >> 4) * 16 + bc) * 2 + ((r >> 3) & 1)) * 8 + (r & 7), E, q);
     }
-  }
-  __syncthreads();
-
-  // V: thread = (dim d, 8-token block kb); b_layout(V, 64, 128): 16-dim band, token block, 8-dim half, dim
+  } else {
+    // V: thread = (dim d, 8-token block kb), reading its 8 tokens of one dim (consecutive lanes read consecutive
+    // dims: 128 contiguous bytes of a row per load); b_layout(V, 64, 128): 16-dim band, token block, 8-dim half, dim
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int item = tid + kQkvThreads * i, d = item & 127, kb = item >> 7;
-    uint32_t u[8], b[8];
-    int32_t q[8];
+    for (int i = 0; i < 4; i++) {
+      const int item = tid + kQkvThreads * i, d = item & 127, kb = item >> 7;
+      uint32_t u[8], b[8];
+      int32_t q[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) u[e] = (uint32_t)vt[(kb * 8 + e) * kVPitch + d] << 16;
-    const uint32_t E = encode_block(u, q, b);
-    if (a.v) {
+      for (int e = 0; e < 8; e++) u[e] = (uint32_t)a.C[(row0 + kb * 8 + e) * a.ldc + col0 + d] << 16;
+      const uint32_t E = encode_block(u, q, b);
+      if (a.v) {
 #pragma unroll
-      for (int e = 0; e < 8; e++) a.v[((int64_t)h * a.M + row0 + kb * 8 + e) * kHeadDim + d] = (uint16_t)b[e];
+        for (int e = 0; e < 8; e++) a.v[((int64_t)h * a.M + row0 + kb * 8 + e) * kHeadDim + d] = (uint16_t)b[e];
+      }
+      if (tiles) stage_block(stage, (((d >> 4) * 8 + kb) * 2 + ((d >> 3) & 1)) * 8 + (d & 7), E, q);
     }
-    if (tiles) stage_block(stage[2], (((d >> 4) * 8 + kb) * 2 + ((d >> 3) & 1)) * 8 + (d & 7), E, q);
   }
   if (!tiles) return;
   __syncthreads();
   const int64_t T = a.M / kTileTokens;
-  for (int c = tid; c < 3 * kTile9 / 16; c += kQkvThreads) {
-    const int part = c / (kTile9 / 16), w = c - part * (kTile9 / 16);
-    uint8_t* dst = part == 0 ? (a.q_tiles ? a.q_tiles + ((int64_t)h * T + t) * kTile9 : nullptr)
-                             : (a.kv_tiles ? a.kv_tiles + (((int64_t)h * T + t) * 2 + (part - 1)) * kTile9 : nullptr);
-    if (dst) *reinterpret_cast<u32x4*>(dst + 16 * w) = *reinterpret_cast<const u32x4*>(&stage[part][16 * w]);
-  }
+  uint8_t* dst = part == 0 ? a.q_tiles + ((int64_t)h * T + t) * kTile9
+                           : a.kv_tiles + (((int64_t)h * T + t) * 2 + (part - 1)) * kTile9;
+  for (int c = tid; c < kTile9 / 16; c += kQkvThreads)
+    *reinterpret_cast<u32x4*>(dst + 16 * c) = *reinterpret_cast<const u32x4*>(&stage[16 * c]);
 }
 
 }  // namespace rl
@@ -162,7 +152,7 @@ extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t he
   a.C = C; a.ldc = ldc; a.M = M; a.heads = heads;
   a.cos = cos; a.sin = sin; a.wq = wq; a.wk = wk;
   a.q_tiles = q_tiles; a.kv_tiles = kv_tiles; a.q = q; a.k = k; a.v = v;
-  const dim3 grid((unsigned)(M / kTileTokens * heads));
+  const dim3 grid((unsigned)(M / kTileTokens * heads * 3));
   hipLaunchKernelGGL(qkv_post_kernel, grid, dim3(kQkvThreads), 0, static_cast<hipStream_t>(stream), a);
   return launch_status("rl_qkv_post");
 }

@@ -163,7 +163,8 @@ int rl_ln_modulate(const uint16_t *x, int64_t ldx, const void *branch, int32_t b
  *   q_tiles  (heads, M/64, 9216 bytes): per head and 64-token tile, to_bfp16(a_layout(Q tile, 64, 128));
  *   kv_tiles (heads, M/64, 2, 9216 bytes): to_bfp16(b_layout(K tile^T, 128, 64)), then to_bfp16(b_layout(V tile, 64,
  *            128)) (the attention kernel's formats, kernels/glue/qkv_post.cc:1-16);
- *   q, k, v  (heads, M, 128) bf16 each: the same quantized values, head major.
+ *   q, k     (heads, M, 128) bf16 each: the same quantized values, head major;
+ *   v        (heads, 128, M) bf16: V transposed (V^T per head, token columns), the layout rl_attention reads.
  * M % 64 == 0, heads >= 1.
  * Replaces the QKV-post artifact (kernels/glue/qkv_design.py:40-118 with qkv_post.cc:134-177) run by
  * run_qkv.qkv32_npu (redline/run_qkv.py:67-82). */
@@ -171,11 +172,28 @@ int rl_qkv_post(const uint16_t *C, int64_t ldc, int64_t M, int32_t heads, const 
                 const uint16_t *wq, const uint16_t *wk, uint8_t *q_tiles, uint8_t *kv_tiles, uint16_t *q, uint16_t *k,
                 uint16_t *v, void *stream);
 
+/* ---- attention over the QKV post pass's output -------------------------------------------------------------------
+ * Per head h and query i: O[i][(h0 + h) * 128 + d] = sum_j P[i][j] V[j][d], P = 2^(S - max) / sum over the visible
+ * keys, S = Q K^T. Q carries the score scale log2(e)/sqrt(128) (as rl_qkv_post's wq does), so S is in log2 units.
+ * Key j is visible to query i when j < nkv and, with lim, j <= lim[i].
+ * Arithmetic: fp32 scores, running max and sums; P rounded to bf16 for the second product; fp32 accumulation; bf16
+ * out. With quantize_out, each 8-dim block of O is quantized to bfp16, making O the out-projection GEMM's RL_A_BF16
+ * operand.
+ * q (heads, nq, 128), k (heads, nk, 128), vt (heads, 128, nk) = V transposed: rl_qkv_post's native outputs, bf16.
+ * o: row major with leading dimension ldo, head h at columns (h0 + h) * 128. lim: nq int32 or NULL.
+ * nq % 128 == 0, nk % 64 == 0, 1 <= nkv <= nk.
+ * Replaces the attention artifacts (kernels/attn/attn_bfp.cc with attn_design.py) run by run_attn.attn_npu
+ * (redline/run_attn.py:67-82) and NPU.run("attn", ...) (redline/forward.py:247, :369-377). */
+int rl_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int32_t heads, int64_t nq, int64_t nk,
+                 int64_t nkv, const int32_t *lim, uint16_t *o, int64_t ldo, int32_t h0, int32_t quantize_out,
+                 void *stream);
+
 /* ---- host-only helpers (no GPU needed) ---------------------------------------------------------------------------- */
 /* Shape/argument checks the entry points run before launching, callable on a machine without a GPU. */
 int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int64_t ld_xo, int32_t a_order,
                    int64_t ld_a, int64_t split_row, int64_t M, int64_t D);
 int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads);
+int rl_validate_attention(int32_t heads, int64_t nq, int64_t nk, int64_t nkv, int64_t ldo, int32_t h0);
 int rl_validate_quantize(int32_t x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int32_t order);
 int rl_validate_gemm(int32_t a_fmt, int64_t lda, int64_t ldc, int64_t M, int64_t N, int64_t K, const rl_epilogue *ep);
 int rl_validate_gemv(int64_t ldx, int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t act);

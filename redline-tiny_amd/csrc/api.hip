@@ -171,4 +171,19 @@ int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads) {
   return rl::ok();
 }
 
+int rl_validate_attention(int32_t heads, int64_t nq, int64_t nk, int64_t nkv, int64_t ldo, int32_t h0) {
+  using rl::fail;
+  if (heads < 1 || heads > 1024) return fail(RL_ERR_SHAPE, "heads %d: need 1..1024", heads);
+  if (nq < 128 || nq % 128 || nq > (1 << 24))
+    return fail(RL_ERR_SHAPE, "nq %lld: need a positive multiple of 128", (long long)nq);
+  if (nk < 64 || nk % 64 || nk > (1 << 24))
+    return fail(RL_ERR_SHAPE, "nk %lld: need a positive multiple of 64", (long long)nk);
+  if (nkv < 1 || nkv > nk) return fail(RL_ERR_SHAPE, "nkv %lld: need 1..nk", (long long)nkv);
+  if (h0 < 0) return fail(RL_ERR_ARG, "h0 < 0");
+  if (ldo < ((int64_t)h0 + heads) * 128 || ldo % 8)
+    return fail(RL_ERR_ALIGN, "ldo %lld: need >= (h0 + heads) * 128 and a multiple of 8", (long long)ldo);
+  if ((int64_t)heads * (nq / 128) > ((int64_t)1 << 31) - 1) return fail(RL_ERR_SHAPE, "too many workgroups");
+  return rl::ok();
+}
+
 }  // extern "C"

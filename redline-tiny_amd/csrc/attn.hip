@@ -1,0 +1,268 @@
+// Attention over the QKV post pass's output: O = softmax2(Q K^T) V per head, flash style (one pass over the keys with
+// a running max and sum), on bf16 MFMA with fp32 scores and accumulation.
+//
+// Replaces the attention artifacts (kernels/attn/attn_bfp.cc with attn_design.py) that run_attn.attn_npu and the DiT
+// step drive (redline/run_attn.py:67-82, redline/forward.py:247, :369-377). As there, Q carries the score scale
+// log2(e)/sqrt(128), so scores are in log2 units and the softmax is 2^(s - max) / sum (attn_bfp.cc:1-12).
+//
+// Workgroup = 4 waves x 32 queries of one head; key blocks of 64 are staged in LDS (double buffered) and read by all
+// four waves. Per wave and key block, with v_mfma_f32_16x16x32_bf16:
+//   S^T (64 keys x 32 queries) = K Q^T: K rows are the A operand, Q^T (kept in registers) the B operand, so each lane
+//     holds 16 keys of one query and the softmax statistics of a query live in one lane column;
+//   O^T (128 dims x 32 queries) += V^T P^T: P^T comes straight out of the S^T registers as the B operand (its 8 keys
+//     per lane are keys 4g..4g+3 and 16+4g..16+4g+3 of a 32-key step), and the V^T A operand is read from LDS with
+//     the same key order. V arrives transposed (rl_qkv_post's V^T output), so no transpose is needed anywhere.
+// K rows in LDS are 256 bytes with the 16-byte chunks XOR-swizzled by key & 15, V^T rows 128 bytes with the 8-byte
+// units swizzled by dim & 15, so that the 16 lanes of an operand read hit distinct banks.
+#include <math.h>
+
+#include "rlbfp.h"
+#include "rlbfp_device.h"
+#include "rlbfp_host.h"
+
+namespace rl {
+
+constexpr int kAtThreads = 256;                 // 4 waves
+constexpr int kAtQW = 32;                       // queries per wave (two 16-query sets)
+constexpr int kAtQ = 4 * kAtQW;                 // 128 queries per workgroup
+constexpr int kAtKB = 64;                       // keys per staged block
+constexpr int kAtHD = 128;                      // head dim
+constexpr int kAtK = kAtKB * kAtHD * 2;         // 16 KB: K block, 64 rows x 256 bytes
+constexpr int kAtStage = 2 * kAtK;              // K block + V^T block (128 rows x 128 bytes)
+
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* vt;
+  uint16_t* o;
+  int64_t ldo;
+  int32_t h0;
+  int32_t heads;
+  int32_t nq;
+  int32_t nk;
+  int32_t nkv;
+  const int32_t* lim;
+  int32_t quantize;
+};
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// two floats -> packed bf16 (round to nearest even; finite inputs)
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const uint32_t a = __float_as_uint(lo), b = __float_as_uint(hi);
+  const uint32_t ra = (a + 0x7FFFu + ((a >> 16) & 1u)) >> 16;
+  const uint32_t rb = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+  return ra | (rb << 16);
+}
+
+__global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kAtStage];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int nqb = a.nq / kAtQ;
+  const int h = blockIdx.x / nqb, qb = blockIdx.x - h * nqb;  // a head's query blocks are neighbours: K/V shared in L2
+  const int q0 = qb * kAtQ + wave * kAtQW;
+  const uint16_t* Qh = a.q + (int64_t)h * a.nq * kAtHD;
+  const uint16_t* Kh = a.k + (int64_t)h * a.nk * kAtHD;
+  const uint16_t* Vh = a.vt + (int64_t)h * kAtHD * a.nk;
+
+  // Q^T as the B operand: set s, 32-dim step st: Q[q0 + 16 s + l16][32 st + 8 lg .. + 7]
+  bf16x8 qB[2][4];
+#pragma unroll
+  for (int s = 0; s < 2; s++)
+#pragma unroll
+    for (int st = 0; st < 4; st++)
+      qB[s][st] = *reinterpret_cast<const bf16x8*>(Qh + (int64_t)(q0 + 16 * s + l16) * kAtHD + 32 * st + 8 * lg);
+  int lim[2];
+#pragma unroll
+  for (int s = 0; s < 2; s++) lim[s] = a.lim ? a.lim[q0 + 16 * s + l16] : 0x7FFFFFFF;
+
+  f32x4 O[2][8];
+#pragma unroll
+  for (int s = 0; s < 2; s++)
+#pragma unroll
+    for (int dg = 0; dg < 8; dg++) O[s][dg] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+
+  // staging of key block kb: K chunks c = tid + 256 i -> (key c / 16, 16-byte chunk c % 16); V^T chunks -> (dim c / 8,
+  // 8 keys c % 8)
+  // buffer loads: one 32-bit lane offset per operand, the chunk and block offsets are wave-uniform
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, (int)((int64_t)a.nk * kAtHD * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, (int)((int64_t)a.nk * kAtHD * 2), 0x00020000);
+  const uint32_t kvo = (uint32_t)((tid >> 4) * kAtHD * 2 + (tid & 15) * 16);  // + i * 16 keys, + block
+  const uint32_t vvo = (uint32_t)((tid >> 3) * a.nk * 2 + (tid & 7) * 16);    // + i * 32 dims, + block
+  u32x4 rk[4], rv[4];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      rk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            krs, kvo, (kb * kAtKB + 16 * i) * kAtHD * 2, 0));
+      rv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            vrs, vvo, 32 * i * a.nk * 2 + kb * kAtKB * 2, 0));
+    }
+  };
+  auto swrite = [&](int stage) {
+    uint8_t* sk = lds + stage * kAtStage;
+    uint8_t* sv = sk + kAtK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = tid + kAtThreads * i;
+      const int key = c >> 4, ch = c & 15;
+      *reinterpret_cast<u32x4*>(sk + key * 256 + ((ch ^ (key & 15)) << 4)) = rk[i];
+      const int dim = c >> 3, u = 2 * (c & 7);
+      *reinterpret_cast<uint2*>(sv + dim * 128 + ((u ^ (dim & 15)) << 3)) = uint2{rv[i].x, rv[i].y};
+      *reinterpret_cast<uint2*>(sv + dim * 128 + (((u + 1) ^ (dim & 15)) << 3)) = uint2{rv[i].z, rv[i].w};
+    }
+  };
+
+  const int nblk = a.nk / kAtKB;
+  gload(0);
+  swrite(0);
+  __syncthreads();
+  for (int j = 0; j < nblk; j++) {
+    const int stage = j & 1;
+    const uint8_t* sk = lds + stage * kAtStage;
+    const uint8_t* sv = sk + kAtK;
+
+    // S^T: S[s][g] lane = keys 16 g + 4 lg + i (i = 0..3) of query 16 s + l16
+    f32x4 S[2][4];
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) S[s][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+#pragma unroll
+      for (int st = 0; st < 4; st++) {
+        const int key = 16 * g + l16, ch = 4 * st + lg;
+        const bf16x8 kA = *reinterpret_cast<const bf16x8*>(sk + key * 256 + ((ch ^ l16) << 4));
+#pragma unroll
+        for (int s = 0; s < 2; s++) S[s][g] = mfma16(kA, qB[s][st], S[s][g]);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // bounds how far LDS reads are hoisted (register pressure)
+    }
+
+    // next block's loads, in flight during the softmax and the second product
+    if (j + 1 < nblk) gload(j + 1);
+
+    // online softmax (base 2) per query; the four lanes l16, l16 + 16, + 32, + 48 hold a query's 64 keys
+    const bool full = (j + 1) * kAtKB <= a.nkv && !a.lim;
+    u32x4 Pb[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      if (!full) {
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int key = j * kAtKB + 16 * g + 4 * lg + i;
+            if (key >= a.nkv || key > lim[s]) S[s][g][i] = -INFINITY;
+          }
+      }
+      float mx = S[s][0][0];
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) mx = fmaxf(mx, S[s][g][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m[s], mx);
+      const bool none = mn == -INFINITY;  // every key so far masked for this query
+      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m[s] - mn);
+      const float base = none ? 0.f : mn;
+      m[s] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float p = __builtin_amdgcn_exp2f(S[s][g][i] - base);
+          S[s][g][i] = p;
+          ps += p;
+        }
+      lsum[s] = lsum[s] * alpha + ps;
+#pragma unroll
+      for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha;
+      // P^T operand for 32-key step c: keys 32c + 4 lg + 0..3 (group 2c), then 32c + 16 + 4 lg + 0..3 (group 2c + 1)
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+        Pb[s][c] = u32x4{pack_bf16(S[s][2 * c][0], S[s][2 * c][1]), pack_bf16(S[s][2 * c][2], S[s][2 * c][3]),
+                         pack_bf16(S[s][2 * c + 1][0], S[s][2 * c + 1][1]),
+                         pack_bf16(S[s][2 * c + 1][2], S[s][2 * c + 1][3])};
+    }
+
+    // O^T += V^T P^T: A = V^T rows 16 dg + l16, keys in the P^T order (8-byte units 8c + lg and 8c + 4 + lg)
+#pragma unroll
+    for (int dg = 0; dg < 8; dg++) {
+      const uint8_t* row = sv + (16 * dg + l16) * 128;
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        const uint2 v0 = *reinterpret_cast<const uint2*>(row + (((8 * c + lg) ^ l16) << 3));
+        const uint2 v1 = *reinterpret_cast<const uint2*>(row + (((8 * c + 4 + lg) ^ l16) << 3));
+        const bf16x8 vA = __builtin_bit_cast(bf16x8, u32x4{v0.x, v0.y, v1.x, v1.y});
+#pragma unroll
+        for (int s = 0; s < 2; s++) O[s][dg] = mfma16(vA, __builtin_bit_cast(bf16x8, Pb[s][c]), O[s][dg]);
+      }
+      if (dg & 1) __builtin_amdgcn_sched_barrier(0);
+    }
+    if (j + 1 < nblk) swrite(stage ^ 1);
+    __syncthreads();
+  }
+
+  // O = O^T / l: lane holds dims 16 dg + 4 lg + i of query q0 + 16 s + l16
+#pragma unroll
+  for (int s = 0; s < 2; s++) {
+    float l = lsum[s];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* orow = a.o + (int64_t)(q0 + 16 * s + l16) * a.ldo + (int64_t)(a.h0 + h) * kAtHD;
+#pragma unroll
+    for (int dg = 0; dg < 8; dg++) {
+      uint32_t u[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) u[i] = __float_as_uint(O[s][dg][i] * inv);
+      if (a.quantize) {
+        // an 8-dim block is split over lanes lg = 2t, 2t + 1 (4 dims each): exchange the exponent with lane ^ 16
+        uint32_t E = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) E = max(E, (u[i] >> 23) & 0xFFu);
+        E = max(E, (uint32_t)__shfl_xor((int)E, 16));
+#pragma unroll
+        for (int i = 0; i < 4; i++) b[i] = quantize_with_exp(u[i], E);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) b[i] = (u[i] + 0x7FFFu + ((u[i] >> 16) & 1u)) >> 16;
+      }
+      *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
+    }
+  }
+}
+
+}  // namespace rl
+
+extern "C" int rl_attention(const uint16_t* q, const uint16_t* k, const uint16_t* vt, int32_t heads, int64_t nq,
+                            int64_t nk, int64_t nkv, const int32_t* lim, uint16_t* o, int64_t ldo, int32_t h0,
+                            int32_t quantize_out, void* stream) {
+  using namespace rl;
+  int s = rl_validate_attention(heads, nq, nk, nkv, ldo, h0);
+  if (s) return s;
+  if (!q || !k || !vt || !o) return fail(RL_ERR_NULL, "q, k, vt or o is NULL");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)vt | (uintptr_t)o) % 16 || (uintptr_t)lim % 4)
+    return fail(RL_ERR_ALIGN, "q, k, vt and o must be 16-byte aligned, lim 4-byte aligned");
+  if ((s = check_device())) return s;
+  AttnArgs a;
+  a.q = q; a.k = k; a.vt = vt; a.o = o; a.ldo = ldo; a.h0 = h0;
+  a.heads = heads; a.nq = (int32_t)nq; a.nk = (int32_t)nk; a.nkv = (int32_t)nkv; a.lim = lim;
+  a.quantize = quantize_out ? 1 : 0;
+  const dim3 grid((unsigned)(heads * (nq / kAtQ)));
+  hipLaunchKernelGGL(attn_kernel, grid, dim3(kAtThreads), 0, static_cast<hipStream_t>(stream), a);
+  return launch_status("rl_attention");
+}

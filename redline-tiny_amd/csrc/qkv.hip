@@ -8,8 +8,8 @@
 //
 // Q and K: thread (token r, 8-dim block bc) holds 8 dims of one token; the 16 threads of a token (16 lanes of a wave)
 // reduce the sum of squares across their lanes. RoPE pairs (2i, 2i + 1) lie inside a block, so each thread rotates
-// its own 4 pairs. V: each thread reads the 8 tokens of one dim that a V block holds. The tile is assembled in LDS
-// in output order and written with 16-byte stores.
+// its own 4 pairs. V: each thread reads the 8 tokens of one dim that a V block holds (and writes them, as one 16-byte
+// store, to the optional V^T output). The tile is assembled in LDS in output order and written with 16-byte stores.
 #include <math.h>
 
 #include "rlbfp.h"
@@ -116,10 +116,9 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; e++) u[e] = (uint32_t)a.C[(row0 + kb * 8 + e) * a.ldc + col0 + d] << 16;
       const uint32_t E = encode_block(u, q, b);
-      if (a.v) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) a.v[((int64_t)h * a.M + row0 + kb * 8 + e) * kHeadDim + d] = (uint16_t)b[e];
-      }
+      if (a.v)  // V^T: the block's 8 tokens are contiguous in row d
+        *reinterpret_cast<u32x4*>(a.v + ((int64_t)h * kHeadDim + d) * a.M + row0 + kb * 8) =
+            u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
       if (tiles) stage_block(stage, (((d >> 4) * 8 + kb) * 2 + ((d >> 3) & 1)) * 8 + (d & 7), E, q);
     }
   }
@@ -145,8 +144,8 @@ extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t he
   if (((uintptr_t)C | (uintptr_t)wq | (uintptr_t)wk | (uintptr_t)q_tiles | (uintptr_t)kv_tiles | (uintptr_t)q |
        (uintptr_t)k) % 16)
     return fail(RL_ERR_ALIGN, "C, wq, wk, the tiles and q / k must be 16-byte aligned");
-  if (((uintptr_t)cos | (uintptr_t)sin) % 8 || (uintptr_t)v % 2)
-    return fail(RL_ERR_ALIGN, "cos / sin must be 8-byte aligned, v 2-byte aligned");
+  if ((uintptr_t)v % 16) return fail(RL_ERR_ALIGN, "v must be 16-byte aligned");
+  if (((uintptr_t)cos | (uintptr_t)sin) % 8) return fail(RL_ERR_ALIGN, "cos / sin must be 8-byte aligned");
   if ((s = check_device())) return s;
   QkvArgs a;
   a.C = C; a.ldc = ldc; a.M = M; a.heads = heads;

@@ -166,6 +166,16 @@ __device__ __forceinline__ uint32_t encode_block(const uint32_t u[8], int32_t q[
   return E;
 }
 
+// One element quantized with a given block exponent E (the block's largest exponent field, found by the caller):
+// the bf16 bits of its bfp16 value. Same arithmetic as encode_block.
+__device__ __forceinline__ uint32_t quantize_with_exp(uint32_t u, uint32_t E) {
+  if (E >= 7u && E <= 254u) {
+    const float qf = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(__uint_as_float(u), 133 - (int)E)), 127.0f);
+    return __float_as_uint(__builtin_amdgcn_ldexpf(qf, (int)E - 133) + 0.0f) >> 16;
+  }
+  return decode_bf16_bits(encode_elem(u, E), E);
+}
+
 // ---- XCD-aware workgroup order -----------------------------------------------------------------------------------
 // Workgroups are dispatched round robin over the 8 XCDs (pid % 8). Map them so that each XCD works on a contiguous
 // range of logical tiles, which then share operands in that XCD's L2.

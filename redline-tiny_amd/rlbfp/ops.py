@@ -1,7 +1,8 @@
 """Tensor-level entry points over librlbfp: quantize / dequantize, the packed-weight GEMM with its fused epilogues,
-grouped GEMMs, the GEMV, the residual + LayerNorm/RMSNorm + modulate pass that produces a GEMM's A, and the QKV post
-pass (per-head RMSNorm + RoPE -> attention tiles). Inputs are torch tensors on a ROCm device (gfx950); outputs are
-allocated here with torch's caching allocator (or passed in) and the work is enqueued on torch's current stream.
+grouped GEMMs, the GEMV, the residual + LayerNorm/RMSNorm + modulate pass that produces a GEMM's A, the QKV post pass
+(per-head RMSNorm + RoPE -> attention tiles) and attention. Inputs are torch tensors on a ROCm device (gfx950);
+outputs are allocated here with torch's caching allocator (or passed in) and the work is enqueued on torch's current
+stream.
 
 Packed streams are uint8 tensors of 9 bytes per 8 values. Packed weights are the bytes redline/pack_weights.py writes:
 to_bfp16(b_layout(W.T, 64, 128)) of a Linear weight W (N, K).
@@ -269,7 +270,8 @@ def qkv_post(C, cos, sin, wq, wk, heads, tiles=True, native=False):
     """Per head of 128 dims: Q = rope(rms(q) * wq), K = rope(rms(k) * wk), V = v, quantized to bfp16 (Q, K in blocks
     of 8 dims, V in blocks of 8 tokens). C (M, 3 * heads * 128) bf16; cos, sin (M, 64) bf16; wq, wk (128,) bf16.
     Returns (q_tiles (heads, M/64, 9216) uint8, kv_tiles (heads, M/64, 2, 9216) uint8) if tiles, else None, None;
-    then (q, k, v) each (heads, M, 128) bf16 if native, else None x 3. See rl_qkv_post in include/rlbfp.h."""
+    then, if native, q and k (heads, M, 128) and v transposed, (heads, 128, M), bf16, else None x 3. See rl_qkv_post
+    in include/rlbfp.h."""
     for t, n in ((C, "C"), (cos, "cos"), (sin, "sin"), (wq, "wq"), (wk, "wk")):
         _dev(t, n)
         if t.dtype != torch.bfloat16:
@@ -284,8 +286,40 @@ def qkv_post(C, cos, sin, wq, wk, heads, tiles=True, native=False):
     T = M // 64
     qt = torch.empty((heads, T, 9216), dtype=torch.uint8, device=C.device) if tiles else None
     kvt = torch.empty((heads, T, 2, 9216), dtype=torch.uint8, device=C.device) if tiles else None
-    q, k, v = ((torch.empty((heads, M, 128), dtype=torch.bfloat16, device=C.device) for _ in range(3)) if native
-               else (None, None, None))
+    q, k, v = ((torch.empty((heads, M, 128), dtype=torch.bfloat16, device=C.device),
+                torch.empty((heads, M, 128), dtype=torch.bfloat16, device=C.device),
+                torch.empty((heads, 128, M), dtype=torch.bfloat16, device=C.device)) if native else (None, None, None))
     L.check(L.lib().rl_qkv_post(_ptr(C), C.stride(0), M, heads, _ptr(cos), _ptr(sin), _ptr(wq), _ptr(wk), _ptr(qt),
                                 _ptr(kvt), _ptr(q), _ptr(k), _ptr(v), _stream(C)))
     return qt, kvt, q, k, v
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------------------------------
+
+def attention(q, k, vt, nkv=None, lim=None, out=None, h0=0, quantize_out=False):
+    """O = softmax2(Q K^T) V per head: q (heads, nq, 128) with the score scale log2(e)/sqrt(128) folded in, k (heads,
+    nk, 128), vt (heads, 128, nk) = V transposed, all bf16 (rl_qkv_post's native outputs). Keys j >= nkv, and j >
+    lim[i] for query i when lim (nq int32) is given, are not visible. Returns out, (nq, ldo) bf16 with head h at
+    columns (h0 + h) * 128 (allocated as (nq, heads * 128) if None); quantize_out rounds each 8-dim block to bfp16.
+    See rl_attention in include/rlbfp.h."""
+    for t, n in ((q, "q"), (k, "k"), (vt, "vt")):
+        _dev(t, n)
+        if t.dtype != torch.bfloat16 or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous bfloat16 tensor")
+    heads, nq, d = q.shape
+    nk = k.shape[1]
+    if d != 128 or k.shape != (heads, nk, 128) or vt.shape != (heads, 128, nk):
+        raise ValueError("q (heads, nq, 128), k (heads, nk, 128) and vt (heads, 128, nk) expected")
+    if out is None:
+        out = torch.empty((nq, (h0 + heads) * 128), dtype=torch.bfloat16, device=q.device)
+    elif out.dtype != torch.bfloat16 or out.shape[0] != nq or out.stride(1) != 1:
+        raise ValueError("out must be (nq, ldo) bfloat16 with unit column stride")
+    if lim is not None:
+        _dev(lim, "lim")
+        if lim.dtype != torch.int32 or lim.numel() != nq or not lim.is_contiguous():
+            raise ValueError("lim must be a contiguous int32 tensor of nq entries")
+    L.check(L.lib().rl_attention(_ptr(q), _ptr(k), _ptr(vt), heads, nq, nk, nk if nkv is None else nkv, _ptr(lim),
+                                 _ptr(out), out.stride(0), h0, 1 if quantize_out else 0, _stream(q)))
+    return out

@@ -144,3 +144,24 @@ def test_qkv_post_null_pointers_rejected_before_any_gpu_call():
     assert lib.rl_qkv_post(None, 384, 64, 1, None, None, None, None, None, None, None, None, None, None) == \
         L.RL_ERR_NULL
     assert lib.rl_qkv_post(16, 384, 64, 1, 16, 16, 16, 16, None, None, None, None, None, None) == L.RL_ERR_NULL
+
+
+@pytest.mark.parametrize("args,code", [
+    ((24, 4352, 4352, 4352, 3072, 0), L.RL_OK),
+    ((32, 4096, 8256, 8224, 4096, 0), L.RL_OK),
+    ((2, 256, 512, 512, 768, 4), L.RL_OK),
+    ((24, 4350, 4352, 4352, 3072, 0), L.RL_ERR_SHAPE),
+    ((24, 4352, 4350, 4350, 3072, 0), L.RL_ERR_SHAPE),
+    ((24, 4352, 4352, 0, 3072, 0), L.RL_ERR_SHAPE),
+    ((24, 4352, 4352, 4353, 3072, 0), L.RL_ERR_SHAPE),
+    ((24, 4352, 4352, 4352, 3000, 0), L.RL_ERR_ALIGN),
+    ((2, 256, 512, 512, 768, 5), L.RL_ERR_ALIGN),
+    ((2, 256, 512, 512, 768, -1), L.RL_ERR_ARG),
+    ((0, 256, 512, 512, 768, 0), L.RL_ERR_SHAPE),
+])
+def test_validate_attention(args, code):
+    assert L.lib().rl_validate_attention(*args) == code
+
+
+def test_attention_null_pointers_rejected_before_any_gpu_call():
+    assert L.lib().rl_attention(None, None, None, 1, 128, 64, 64, None, None, 128, 0, 0, None) == L.RL_ERR_NULL

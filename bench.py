@@ -13,8 +13,8 @@ CUs, then the last 256 rows in 128-row tiles), timed together. Kernel times are 
 launch stream.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
 rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
-produces the up GEMM's A (4352 x 3072) and the QKV post pass (4352 tokens x 24 heads) in GB/s against HBM; and the
-CPU baseline (the oracle's numpy restatement of the reference CPU path on a row sample of the same workload).
+produces the up GEMM's A (4352 x 3072) and the QKV post pass (4352 tokens x 24 heads) in GB/s against HBM; attention
+over 4352 tokens x 24 heads in TFLOP/s (torch's SDPA beside it); and the CPU baseline (the oracle's numpy restatement of the reference CPU path on a row sample of the same workload).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--copy-probe MB] [--sustain SECONDS]
 """
@@ -196,6 +196,7 @@ def gpu_bench(steps, warmup):
         "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
         "ln": ln_bench(dev),
         "qkv": qkv_bench(dev),
+        "attn": attn_bench(dev),
     }
 
 
@@ -265,6 +266,39 @@ def graph_us(call, warm, per_graph, reps):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def attn_bench(dev, heads=24, per_graph=10, reps=3):
+    """Attention over the benchmark's M (4352 tokens, 24 heads of 128 = hidden 3072): Q (score scale folded in), K,
+    V^T bf16 in, bf16 O out (4 * heads * M^2 * 128 FLOP); HIP-graph replays. torch's bf16 scaled_dot_product_attention
+    of the same shape is timed beside it as a reference point."""
+    import torch
+
+    from rlbfp import ops
+
+    g = torch.Generator(device=dev).manual_seed(13)
+    q = (torch.randn((heads, M, 128), generator=g, device=dev) * 0.1275).to(torch.bfloat16)
+    k = torch.randn((heads, M, 128), generator=g, device=dev).to(torch.bfloat16)
+    vt = torch.randn((heads, 128, M), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty((M, heads * 128), dtype=torch.bfloat16, device=dev)
+    us = graph_us(lambda i: ops.attention(q, k, vt, out=out), 3, per_graph, reps)
+    flops = 4.0 * heads * M * M * 128
+    qs, ks, vs = q.unsqueeze(0), k.unsqueeze(0), vt.transpose(1, 2).contiguous().unsqueeze(0)
+    f = torch.nn.functional.scaled_dot_product_attention
+    for _ in range(3):
+        f(qs, ks, vs)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(per_graph):
+        f(qs, ks, vs)
+    e1.record()
+    torch.cuda.synchronize()
+    us_t = e0.elapsed_time(e1) * 1e3 / per_graph
+    tf = flops / (us * 1e-6) / 1e12
+    return {"shape": [heads, M, M, 128], "us": round(us, 2), "tflops": round(tf, 1),
+            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "torch_sdpa_us": round(us_t, 2),
+            "torch_sdpa_tflops": round(flops / (us_t * 1e-6) / 1e12, 1)}
 
 
 def qkv_bench(dev, heads=24, sets=3, per_graph=30, reps=4):
@@ -486,6 +520,7 @@ def main():
                  "copies": 6},
         "ln_modulate": r["ln"],
         "qkv_post": r["qkv"],
+        "attention": r["attn"],
     }
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(r["host"], r["p_up"], r["p_down"])
     print(json.dumps(line), flush=True)

@@ -51,12 +51,12 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// two floats -> packed bf16 (round to nearest even; finite inputs)
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats -> packed bf16, round to nearest even (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  const uint32_t a = __float_as_uint(lo), b = __float_as_uint(hi);
-  const uint32_t ra = (a + 0x7FFFu + ((a >> 16) & 1u)) >> 16;
-  const uint32_t rb = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-  return ra | (rb << 16);
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
@@ -188,8 +188,10 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
           ps += p;
         }
       lsum[s] = lsum[s] * alpha + ps;
+      if (__any(alpha != 1.f)) {  // the running max moved for some query of this set (wave-uniform branch)
 #pragma unroll
-      for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha;
+        for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha;
+      }
       // P^T operand for 32-key step c: keys 32c + 4 lg + 0..3 (group 2c), then 32c + 16 + 4 lg + 0..3 (group 2c + 1)
 #pragma unroll
       for (int c = 0; c < 2; c++)
@@ -237,11 +239,12 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
         E = max(E, (uint32_t)__shfl_xor((int)E, 16));
 #pragma unroll
         for (int i = 0; i < 4; i++) b[i] = quantize_with_exp(u[i], E);
+        *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
       } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) b[i] = (u[i] + 0x7FFFu + ((u[i] >> 16) & 1u)) >> 16;
+        *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) =
+            uint2{pack_bf16(__uint_as_float(u[0]), __uint_as_float(u[1])),
+                  pack_bf16(__uint_as_float(u[2]), __uint_as_float(u[3]))};
       }
-      *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
     }
   }
 }

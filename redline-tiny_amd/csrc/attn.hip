@@ -53,6 +53,29 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
+// Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the lane groups holding one query's keys), with the
+// gfx950 row-swap permutes instead of LDS round trips: permlane16_swap(x, x) yields rows {0,0,2,2} and {1,1,3,3},
+// permlane32_swap(x, x) rows {0,1,0,1} and {2,3,2,3}.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max4(float v) {
+  v = max_xor16(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum4(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// A rebase of the running max happens only when a block's scores exceed it by more than this many log2 units, so
+// most blocks skip the rescale of O; P then stays below 2^8 (exact enough in fp32, rounded to bf16 like any P).
+constexpr float kAtRebase = 8.0f;
+
 // two floats -> packed bf16, round to nearest even (one v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   const bf16x2 v = {(__bf16)lo, (__bf16)hi};
@@ -131,12 +154,15 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
     const uint8_t* sk = lds + stage * kAtStage;
     const uint8_t* sv = sk + kAtK;
 
-    // S^T: S[s][g] lane = keys 16 g + 4 lg + i (i = 0..3) of query 16 s + l16
+    // S^T - m: S[s][g] lane = keys 16 g + 4 lg + i (i = 0..3) of query 16 s + l16, minus the query's running max
+    // (the accumulators start at -m; 0 while no key has been visible)
     f32x4 S[2][4];
 #pragma unroll
-    for (int s = 0; s < 2; s++)
+    for (int s = 0; s < 2; s++) {
+      const float nb = m[s] == -INFINITY ? 0.f : -m[s];
 #pragma unroll
-      for (int g = 0; g < 4; g++) S[s][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < 4; g++) S[s][g] = f32x4{nb, nb, nb, nb};
+    }
 #pragma unroll
     for (int g = 0; g < 4; g++) {
 #pragma unroll
@@ -171,33 +197,40 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
       for (int g = 0; g < 4; g++)
 #pragma unroll
         for (int i = 0; i < 4; i++) mx = fmaxf(mx, S[s][g][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = fmaxf(m[s], mx);
-      const bool none = mn == -INFINITY;  // every key so far masked for this query
-      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m[s] - mn);
-      const float base = none ? 0.f : mn;
-      m[s] = mn;
-      float ps = 0.f;
+      mx = max4(mx);
+      // rebase when the query has no reference yet, or this block exceeds it by more than kAtRebase
+      const bool need = mx != -INFINITY && (m[s] == -INFINITY || mx > kAtRebase);
+      const float delta = need ? mx : 0.f;
+      if (__any(need)) {  // wave-uniform branch, rare after the first block
+        const float alpha = __builtin_amdgcn_exp2f(-delta);
+        m[s] = need ? (m[s] == -INFINITY ? mx : m[s] + mx) : m[s];
+        lsum[s] *= alpha;
+#pragma unroll
+        for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha;
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) S[s][g][i] -= delta;
+      }
 #pragma unroll
       for (int g = 0; g < 4; g++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float p = __builtin_amdgcn_exp2f(S[s][g][i] - base);
-          S[s][g][i] = p;
-          ps += p;
-        }
-      lsum[s] = lsum[s] * alpha + ps;
-      if (__any(alpha != 1.f)) {  // the running max moved for some query of this set (wave-uniform branch)
-#pragma unroll
-        for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha;
-      }
+        for (int i = 0; i < 4; i++) S[s][g][i] = __builtin_amdgcn_exp2f(S[s][g][i]);
       // P^T operand for 32-key step c: keys 32c + 4 lg + 0..3 (group 2c), then 32c + 16 + 4 lg + 0..3 (group 2c + 1)
 #pragma unroll
       for (int c = 0; c < 2; c++)
         Pb[s][c] = u32x4{pack_bf16(S[s][2 * c][0], S[s][2 * c][1]), pack_bf16(S[s][2 * c][2], S[s][2 * c][3]),
                          pack_bf16(S[s][2 * c + 1][0], S[s][2 * c + 1][1]),
                          pack_bf16(S[s][2 * c + 1][2], S[s][2 * c + 1][3])};
+      // the row sum from the same bf16 P the second product uses
+      const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          const uint32_t pw = Pb[s][c][w];  // a scalar copy: bit_cast of a vector-element lvalue reads element 0
+          lsum[s] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw), one, lsum[s], false);
+        }
     }
 
     // O^T += V^T P^T: A = V^T rows 16 dg + l16, keys in the P^T order (8-byte units 8c + lg and 8c + 4 + lg)
@@ -221,9 +254,7 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
   // O = O^T / l: lane holds dims 16 dg + 4 lg + i of query q0 + 16 s + l16
 #pragma unroll
   for (int s = 0; s < 2; s++) {
-    float l = lsum[s];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = sum4(lsum[s]);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t* orow = a.o + (int64_t)(q0 + 16 * s + l16) * a.ldo + (int64_t)(a.h0 + h) * kAtHD;
 #pragma unroll
@@ -236,7 +267,8 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
         uint32_t E = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) E = max(E, (u[i] >> 23) & 0xFFu);
-        E = max(E, (uint32_t)__shfl_xor((int)E, 16));
+        const auto r = __builtin_amdgcn_permlane16_swap(E, E, false, false);
+        E = max((uint32_t)r[0], (uint32_t)r[1]);
 #pragma unroll
         for (int i = 0; i < 4; i++) b[i] = quantize_with_exp(u[i], E);
         *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};

@@ -112,9 +112,13 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
     for (int dg = 0; dg < 8; dg++) O[s][dg] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
 
-  // staging of key block kb: K chunks c = tid + 256 i -> (key c / 16, 16-byte chunk c % 16); V^T chunks -> (dim c / 8,
-  // 8 keys c % 8)
-  // buffer loads: one 32-bit lane offset per operand, the chunk and block offsets are wave-uniform
+  // LDS: K buffers 0, 1, then V^T buffers 0, 1 (16 KB each). K runs one key block ahead of V: iteration j computes
+  // S(j + 1) from K buffer (j + 1) % 2 while O accumulates P(j) V(j) from V buffer j % 2, and the softmax of block
+  // j + 1 (VALU) can be scheduled between the P(j) V(j) MFMAs.
+  uint8_t* const kbuf = lds;
+  uint8_t* const vbuf = lds + 2 * kAtK;
+  // staging: K chunks c = tid + 256 i -> (key c / 16, 16-byte chunk c % 16); V^T chunks -> (dim c / 8, 8 keys c % 8);
+  // buffer loads with one 32-bit lane offset per operand, the chunk and block offsets wave-uniform
   const __amdgpu_buffer_rsrc_t krs =
       __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, (int)((int64_t)a.nk * kAtHD * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs =
@@ -122,41 +126,41 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
   const uint32_t kvo = (uint32_t)((tid >> 4) * kAtHD * 2 + (tid & 15) * 16);  // + i * 16 keys, + block
   const uint32_t vvo = (uint32_t)((tid >> 3) * a.nk * 2 + (tid & 7) * 16);    // + i * 32 dims, + block
   u32x4 rk[4], rv[4];
-  auto gload = [&](int kb) {
+  auto load_k = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 4; i++)
       rk[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             krs, kvo, (kb * kAtKB + 16 * i) * kAtHD * 2, 0));
+  };
+  auto load_v = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
       rv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                             vrs, vvo, 32 * i * a.nk * 2 + kb * kAtKB * 2, 0));
-    }
   };
-  auto swrite = [&](int stage) {
-    uint8_t* sk = lds + stage * kAtStage;
-    uint8_t* sv = sk + kAtK;
+  auto store_k = [&](int buf) {
+    uint8_t* sk = kbuf + buf * kAtK;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int c = tid + kAtThreads * i;
-      const int key = c >> 4, ch = c & 15;
+      const int c = tid + kAtThreads * i, key = c >> 4, ch = c & 15;
       *reinterpret_cast<u32x4*>(sk + key * 256 + ((ch ^ (key & 15)) << 4)) = rk[i];
-      const int dim = c >> 3, u = 2 * (c & 7);
+    }
+  };
+  auto store_v = [&](int buf) {
+    uint8_t* sv = vbuf + buf * kAtK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = tid + kAtThreads * i, dim = c >> 3, u = 2 * (c & 7);
       *reinterpret_cast<uint2*>(sv + dim * 128 + ((u ^ (dim & 15)) << 3)) = uint2{rv[i].x, rv[i].y};
       *reinterpret_cast<uint2*>(sv + dim * 128 + (((u + 1) ^ (dim & 15)) << 3)) = uint2{rv[i].z, rv[i].w};
     }
   };
 
-  const int nblk = a.nk / kAtKB;
-  gload(0);
-  swrite(0);
-  __syncthreads();
-  for (int j = 0; j < nblk; j++) {
-    const int stage = j & 1;
-    const uint8_t* sk = lds + stage * kAtStage;
-    const uint8_t* sv = sk + kAtK;
-
-    // S^T - m: S[s][g] lane = keys 16 g + 4 lg + i (i = 0..3) of query 16 s + l16, minus the query's running max
-    // (the accumulators start at -m; 0 while no key has been visible)
-    f32x4 S[2][4];
+  // S^T - m of key block b: S[s][g] lane = keys 16 g + 4 lg + i (i = 0..3) of query 16 s + l16, minus the query's
+  // running max (the accumulators start at -m; 0 while no key has been visible)
+  f32x4 S[2][4];
+  auto scores = [&](int b) {
+    const uint8_t* sk = kbuf + (b & 1) * kAtK;
 #pragma unroll
     for (int s = 0; s < 2; s++) {
       const float nb = m[s] == -INFINITY ? 0.f : -m[s];
@@ -172,15 +176,14 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < 2; s++) S[s][g] = mfma16(kA, qB[s][st], S[s][g]);
       }
-      __builtin_amdgcn_sched_barrier(0);  // bounds how far LDS reads are hoisted (register pressure)
     }
+  };
 
-    // next block's loads, in flight during the softmax and the second product
-    if (j + 1 < nblk) gload(j + 1);
-
-    // online softmax (base 2) per query; the four lanes l16, l16 + 16, + 32, + 48 hold a query's 64 keys
-    const bool full = (j + 1) * kAtKB <= a.nkv && !a.lim;
-    u32x4 Pb[2][2];
+  // online softmax (base 2) of block b: P^T -> Pb (bf16), row sums into lsum; alpha[s] is the factor O must take
+  // (after its P V products of the previous block) when the running max was rebased, rebased[s] whether any lane of
+  // the set did. The four lanes l16, l16 + 16, + 32, + 48 hold a query's 64 keys.
+  auto softmax = [&](int b, u32x4 (&Pb)[2][2], float (&alpha)[2], bool (&rebased)[2]) {
+    const bool full = (b + 1) * kAtKB <= a.nkv && !a.lim;
 #pragma unroll
     for (int s = 0; s < 2; s++) {
       if (!full) {
@@ -188,7 +191,7 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
         for (int g = 0; g < 4; g++)
 #pragma unroll
           for (int i = 0; i < 4; i++) {
-            const int key = j * kAtKB + 16 * g + 4 * lg + i;
+            const int key = b * kAtKB + 16 * g + 4 * lg + i;
             if (key >= a.nkv || key > lim[s]) S[s][g][i] = -INFINITY;
           }
       }
@@ -201,12 +204,12 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
       // rebase when the query has no reference yet, or this block exceeds it by more than kAtRebase
       const bool need = mx != -INFINITY && (m[s] == -INFINITY || mx > kAtRebase);
       const float delta = need ? mx : 0.f;
-      if (__any(need)) {  // wave-uniform branch, rare after the first block
-        const float alpha = __builtin_amdgcn_exp2f(-delta);
+      alpha[s] = 1.f;
+      rebased[s] = __any(need);
+      if (rebased[s]) {  // wave-uniform branch, rare after the first block
+        alpha[s] = __builtin_amdgcn_exp2f(-delta);
         m[s] = need ? (m[s] == -INFINITY ? mx : m[s] + mx) : m[s];
-        lsum[s] *= alpha;
-#pragma unroll
-        for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha;
+        lsum[s] *= alpha[s];
 #pragma unroll
         for (int g = 0; g < 4; g++)
 #pragma unroll
@@ -232,8 +235,11 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
           lsum[s] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw), one, lsum[s], false);
         }
     }
+  };
 
-    // O^T += V^T P^T: A = V^T rows 16 dg + l16, keys in the P^T order (8-byte units 8c + lg and 8c + 4 + lg)
+  // O^T += V^T P^T of block b: A = V^T rows 16 dg + l16, keys in the P^T order (8-byte units 8c + lg, 8c + 4 + lg)
+  auto pv = [&](int b, const u32x4 (&Pb)[2][2]) {
+    const uint8_t* sv = vbuf + (b & 1) * kAtK;
 #pragma unroll
     for (int dg = 0; dg < 8; dg++) {
       const uint8_t* row = sv + (16 * dg + l16) * 128;
@@ -245,11 +251,45 @@ __global__ __launch_bounds__(kAtThreads, 2) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < 2; s++) O[s][dg] = mfma16(vA, __builtin_bit_cast(bf16x8, Pb[s][c]), O[s][dg]);
       }
-      if (dg & 1) __builtin_amdgcn_sched_barrier(0);
     }
-    if (j + 1 < nblk) swrite(stage ^ 1);
+  };
+
+  const int nblk = a.nk / kAtKB;
+  load_k(0);
+  load_v(0);
+  store_k(0);
+  store_v(0);
+  load_k(min(1, nblk - 1));
+  store_k(1);
+  __syncthreads();
+  u32x4 Pb[2][2];
+  float alpha[2];
+  bool rebased[2];
+  scores(0);
+  softmax(0, Pb, alpha, rebased);  // O is still 0: no rescale
+  // Every load and store below is unconditional: past the last block they repeat block nblk - 1 into a buffer that is
+  // not read again, which keeps the loop free of branches around memory operations.
+  for (int j = 0; j + 1 < nblk; j++) {
+    load_v(j + 1);
+    load_k(min(j + 2, nblk - 1));
+    scores(j + 1);
+    pv(j, Pb);
+    u32x4 Pn[2][2];
+    softmax(j + 1, Pn, alpha, rebased);
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      if (rebased[s]) {  // O has P(j) V(j) now; a rebase at block j + 1 applies to all of it
+#pragma unroll
+        for (int dg = 0; dg < 8; dg++) O[s][dg] *= alpha[s];
+      }
+#pragma unroll
+      for (int c = 0; c < 2; c++) Pb[s][c] = Pn[s][c];
+    }
+    store_v((j + 1) & 1);  // V buffer (j + 1) % 2 held V(j - 1), read in iteration j - 1
+    store_k(j & 1);        // K buffer j % 2 held K(j), read in iteration j - 1
     __syncthreads();
   }
+  pv(nblk - 1, Pb);
 
   // O = O^T / l: lane holds dims 16 dg + 4 lg + i of query q0 + 16 s + l16
 #pragma unroll

@@ -54,13 +54,6 @@ struct GemmArgs {
   int32_t n;
 };
 
-// Waits until at most N vector-memory loads of this wave are outstanding (s_waitcnt vmcnt(N), gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 // Scheduling pattern for one K step of the pipelined loop (two halves of 64 MFMAs, 16 A reads and ~104 decode
 // VALU ops each): four A reads up front, then per row fragment its 4 MFMAs with one A read (four fragments ahead)
 // and seven VALU ops between them, so that neither LDS latency nor the decode stalls the matrix pipe.

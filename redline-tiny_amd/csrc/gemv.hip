@@ -24,9 +24,11 @@ __device__ __forceinline__ float silu_v(float x) {
 
 // Workgroup = one 16-column group g of the b_layout (N tile g / 8, super-block g % 8), all of K. Wave w takes the
 // iterations it = w, w + 2, ... of 8 K tiles each. An iteration's 8 x 1152 bytes are read with 9 coalesced 1 KB
-// loads into registers, one iteration ahead; they pass through the wave's own 9 KB of LDS, from which lane
-// l = (run, br) = (l/8, l%8) reads its 16 blocks (K rows br*8..+7 of K tile 8 it + run, 16 columns) as 144 aligned
-// bytes at offset 144 l (a 36-dword stride, which covers all banks).
+// loads; they pass through the wave's own 9 KB of LDS, from which lane l = (run, br) = (l/8, l%8) reads its 16 blocks
+// (K rows br*8..+7 of K tile 8 it + run, 16 columns) as 144 aligned bytes at offset 144 l (a 36-dword stride, which
+// covers all banks). Iterations go in groups of three whose loads are all issued at once (the first straight into
+// LDS, the other two into registers), which is all of a wave's 27 KB at K = 3072, and act(x) for the three is
+// quantized while the blocks are in flight: the math left behind the last bytes to arrive is the block products.
 //
 // act(x) of the lane's 8 K rows is quantized to one bfp16 block per row of x (E = largest float32 exponent field,
 // q = rint(v * 2^(133-E)) clipped to [-128, 127], as the activation encoder does), so that each weight block
@@ -58,17 +60,26 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv
     const int ci = 64 * i + lane;
     voff[i] = (uint32_t)(((int64_t)nt * KT + ci / 72) * 9216 + sbc * 1152 + 16 * (ci % 72));
   }
-  u32x4 w[S][9], xs[S][M];
-  auto gload = [&](int idx, u32x4 (&dw)[9], u32x4 (&dx)[M]) {
+  u32x4 w[S][9], xs[S][M], x0[M];
+  // x rows of iteration idx (M loads, unconditional: past the last K tile they read the clamped tile)
+  auto xload = [&](int idx, u32x4 (&dx)[M]) {
+    const int kt = min(8 * (wave + kVWaves * idx) + run, KT - 1);
+#pragma unroll
+    for (int m = 0; m < M; m++) dx[m] = *reinterpret_cast<const u32x4*>(x + m * ldx + kt * 64 + br * 8);
+  };
+  auto wload = [&](int idx, u32x4 (&dw)[9]) {
     const int it = wave + kVWaves * idx;
 #pragma unroll
     for (int i = 0; i < 9; i++)
       dw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], it * 8 * 9216, 0));
-    const int kt = 8 * it + run;
-    if (kt < KT) {
+  };
+  // iteration 0 goes straight to the wave's LDS buffer (lane l of load i lands at 1024 i + 16 l, the staged order)
+  auto dma = [&](int idx) {
+    const int it = wave + kVWaves * idx;
 #pragma unroll
-      for (int m = 0; m < M; m++) dx[m] = *reinterpret_cast<const u32x4*>(x + m * ldx + kt * 64 + br * 8);
-    }
+    for (int i = 0; i < 9; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)&buf[wave][1024 * i], 16,
+                                               voff[i], it * 8 * 9216, 0, 0);
   };
 
   float part[M][16];
@@ -77,36 +88,48 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv
 #pragma unroll
     for (int j = 0; j < 16; j++) part[m][j] = 0.f;
 
-  auto body = [&](int idx, const u32x4 (&dw)[9], const u32x4 (&xv)[M]) {
-    const int kt = 8 * (wave + kVWaves * idx) + run;
-    // realign through LDS: the coalesced chunks go in as loaded, each lane takes out its 144-byte run of blocks
+  // realign through LDS: the coalesced chunks go in as loaded, each lane takes out its 144-byte run of blocks
+  auto stage = [&](const u32x4 (&dw)[9]) {
 #pragma unroll
     for (int i = 0; i < 9; i++) *reinterpret_cast<u32x4*>(&buf[wave][1024 * i + 16 * lane]) = dw[i];
+  };
+  // act(x) of iteration idx's 8 K rows, quantized to one bfp16 block per row of x. Past the last K tile (whose
+  // blocks may be the next N tile's) the x block is zero, so those products are exactly 0 and the block loop runs
+  // without a branch.
+  struct XQ {
+    uint32_t q[M][2];
+    int e[M];
+  };
+  auto quant = [&](int idx, const u32x4 (&xv)[M], XQ& o) {
+    const int kt = 8 * (wave + kVWaves * idx) + run;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint32_t xw[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
+      float v[8];
+      uint32_t e = 0;
+#pragma unroll
+      for (int r = 0; r < 8; r++) {
+        const float t = __uint_as_float(r & 1 ? xw[r >> 1] & 0xFFFF0000u : xw[r >> 1] << 16);
+        v[r] = SILU ? silu_v(t) : t;
+        e = max(e, (__float_as_uint(v[r]) >> 23) & 0xFFu);
+      }
+      o.e[m] = (int)e;
+      int qi[8];
+#pragma unroll
+      for (int r = 0; r < 8; r++)
+        qi[r] = (int)fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(v[r], 133 - (int)e)), 127.0f);
+      o.q[m][0] = (qi[0] & 0xFF) | ((qi[1] & 0xFF) << 8) | ((qi[2] & 0xFF) << 16) | ((uint32_t)qi[3] << 24);
+      o.q[m][1] = (qi[4] & 0xFF) | ((qi[5] & 0xFF) << 8) | ((qi[6] & 0xFF) << 16) | ((uint32_t)qi[7] << 24);
+      if (kt >= KT) o.q[m][0] = o.q[m][1] = 0u;
+    }
+  };
+  auto body = [&](const XQ& xq) {
+    const auto& qx = xq.q;
+    const auto& ex = xq.e;
     u32x4 cur[9];
 #pragma unroll
     for (int i = 0; i < 9; i++) cur[i] = *reinterpret_cast<const u32x4*>(&buf[wave][144 * lane + 16 * i]);
-    if (kt < KT) {
-      uint32_t qx[M][2];
-      int ex[M];
-#pragma unroll
-      for (int m = 0; m < M; m++) {
-        const uint32_t xw[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
-        float v[8];
-        uint32_t e = 0;
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-          const float t = __uint_as_float(r & 1 ? xw[r >> 1] & 0xFFFF0000u : xw[r >> 1] << 16);
-          v[r] = SILU ? silu_v(t) : t;
-          e = max(e, (__float_as_uint(v[r]) >> 23) & 0xFFu);
-        }
-        ex[m] = (int)e;
-        int qi[8];
-#pragma unroll
-        for (int r = 0; r < 8; r++)
-          qi[r] = (int)fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(v[r], 133 - (int)e)), 127.0f);
-        qx[m][0] = (qi[0] & 0xFF) | ((qi[1] & 0xFF) << 8) | ((qi[2] & 0xFF) << 16) | ((uint32_t)qi[3] << 24);
-        qx[m][1] = (qi[4] & 0xFF) | ((qi[5] & 0xFF) << 8) | ((qi[6] & 0xFF) << 16) | ((uint32_t)qi[7] << 24);
-      }
+    {
       const uint32_t* wd = reinterpret_cast<const uint32_t*>(cur);
 #pragma unroll
       for (int j = 0; j < 16; j++) {
@@ -125,18 +148,45 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv
     }
   };
 
-  // ring of S register slots, loads S - 1 iterations ahead of the math
+  // Iterations go in groups of three, all requested at once: the first into LDS, the other two into the register
+  // slots. A group is straight-line code, so each wait is for its own iteration only (with uses under a branch the
+  // compiler would sink the loads into it). Loads past this wave's iterations are safe: buffer loads beyond the
+  // stream return zeros, x loads use a clamped K tile.
+  for (int g0 = 0; g0 < mine; g0 += 1 + S) {
+    // issue order (fenced, and the waits below count on it): the three iterations' x rows, then the blocks of
+    // the first (into LDS), the second and the third
+    xload(g0, x0);
 #pragma unroll
-  for (int s0 = 0; s0 < S - 1; s0++)
-    if (s0 < mine) gload(s0, w[s0], xs[s0]);
-  for (int base = 0; base < mine; base += S) {
+    for (int s0 = 0; s0 < S; s0++) xload(g0 + 1 + s0, xs[s0]);
+    __builtin_amdgcn_sched_barrier(0);
+    dma(g0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s0 = 0; s0 < S; s0++) {
-      const int idx = base + s0;
-      if (idx < mine) {
-        if (idx + S - 1 < mine) gload(idx + S - 1, w[(s0 + S - 1) % S], xs[(s0 + S - 1) % S]);
-        body(idx, w[s0], xs[s0]);
-      }
+      wload(g0 + 1 + s0, w[s0]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the x rows land first: for up to 4 rows of x, act(x) of all three iterations is quantized while the blocks
+    // are still in flight (more rows would not fit the registers; they are quantized per iteration)
+    constexpr bool kEarly = M <= 4;
+    XQ xq[1 + S];
+    if constexpr (kEarly) {
+      wait_vm<9 * (1 + S)>();
+      quant(g0, x0, xq[0]);
+#pragma unroll
+      for (int s0 = 0; s0 < S; s0++) quant(g0 + 1 + s0, xs[s0], xq[1 + s0]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vm<9 * S>();  // the group's first iteration has landed
+    if constexpr (!kEarly) quant(g0, x0, xq[0]);
+    body(xq[0]);
+    // iterations past this wave's last one have every K tile >= KT, so their x blocks are zero and they add 0
+#pragma unroll
+    for (int s0 = 0; s0 < S; s0++) {
+      __builtin_amdgcn_sched_barrier(0);  // one iteration's math before the next one's wait
+      stage(w[s0]);
+      if constexpr (!kEarly) quant(g0 + 1 + s0, xs[s0], xq[1 + s0]);
+      body(xq[1 + s0]);
     }
   }
 

@@ -176,6 +176,13 @@ __device__ __forceinline__ uint32_t quantize_with_exp(uint32_t u, uint32_t E) {
   return decode_bf16_bits(encode_elem(u, E), E);
 }
 
+// Waits until at most N vector-memory loads of this wave are outstanding (s_waitcnt vmcnt(N), gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // ---- XCD-aware workgroup order -----------------------------------------------------------------------------------
 // Workgroups are dispatched round robin over the 8 XCDs (pid % 8). Map them so that each XCD works on a contiguous
 // range of logical tiles, which then share operands in that XCD's L2.

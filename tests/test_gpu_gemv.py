@@ -12,7 +12,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("M,K,N,act", [(1, 3072, 18432, "silu"), (2, 4096, 16384, "silu"), (8, 192, 384, None),
-                                       (3, 640, 1024, "silu"), (1, 64, 128, None)])
+                                       (3, 640, 1024, "silu"), (1, 64, 128, None), (4, 1536, 2048, "silu"),
+                                       (5, 5120, 256, None), (6, 704, 512, "silu"), (7, 2560, 384, None)])
 def test_gemv(dev, M, K, N, act):
     rng = np.random.default_rng(M + K)
     x = F.bf16_round(rng.standard_normal((M, K)).astype(np.float32))

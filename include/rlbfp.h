@@ -188,6 +188,21 @@ int rl_attention(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int32
                  int64_t nkv, const int32_t *lim, uint16_t *o, int64_t ldo, int32_t h0, int32_t quantize_out,
                  void *stream);
 
+/* rl_attention with a caller's workspace (device memory, 16-byte aligned), which lets the launch split work along the
+ * keys: the tasks (head, 128-query block) that fill whole rounds of the GPU's resident workgroups run whole, and when
+ * the tasks left over fill at most 4/5 of a round their key blocks are spread over every resident workgroup. A task
+ * cut into pieces leaves fp32 partials (unnormalised O, running max, sum) in the workspace, merged in piece order by
+ * a second launch on the same stream (the result does not depend on timing). Same arguments and results as
+ * rl_attention; summation order differs from the unsplit launch within fp32 rounding.
+ * workspace NULL: every task runs whole. workspace_bytes below rl_attention_workspace_bytes(): RL_ERR_WORKSPACE.
+ * Calls that share a workspace on different streams race. Same reference interface as rl_attention. */
+int rl_attention_ws(const uint16_t *q, const uint16_t *k, const uint16_t *vt, int32_t heads, int64_t nq, int64_t nk,
+                    int64_t nkv, const int32_t *lim, uint16_t *o, int64_t ldo, int32_t h0, int32_t quantize_out,
+                    void *workspace, int64_t workspace_bytes, void *stream);
+/* Workspace bytes rl_attention_ws needs for this shape on the current device (0: no split for this shape; -1: the
+ * shape is invalid). Without a usable device the plan assumes 256 compute units. */
+int64_t rl_attention_workspace_bytes(int32_t heads, int64_t nq, int64_t nk);
+
 /* ---- host-only helpers (no GPU needed) ---------------------------------------------------------------------------- */
 /* Shape/argument checks the entry points run before launching, callable on a machine without a GPU. */
 int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int64_t ld_xo, int32_t a_order,

@@ -58,6 +58,8 @@ SIGNATURES = {
                                       _I64, _P]),
     "rl_qkv_post": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "rl_attention": (ctypes.c_int, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _P, _I64, _I32, _I32, _P]),
+    "rl_attention_ws": (ctypes.c_int, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _I64, _P]),
+    "rl_attention_workspace_bytes": (ctypes.c_int64, [_I32, _I64, _I64]),
     "rl_validate_quantize": (ctypes.c_int, [_I32, _I64, _I64, _I64, _I32]),
     "rl_validate_gemm": (ctypes.c_int, [_I32, _I64, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue)]),
     "rl_validate_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I32]),

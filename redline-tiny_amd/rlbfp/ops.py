@@ -298,12 +298,14 @@ def qkv_post(C, cos, sin, wq, wk, heads, tiles=True, native=False):
 # attention
 # ---------------------------------------------------------------------------------------------------------------
 
-def attention(q, k, vt, nkv=None, lim=None, out=None, h0=0, quantize_out=False):
+def attention(q, k, vt, nkv=None, lim=None, out=None, h0=0, quantize_out=False, split=True):
     """O = softmax2(Q K^T) V per head: q (heads, nq, 128) with the score scale log2(e)/sqrt(128) folded in, k (heads,
     nk, 128), vt (heads, 128, nk) = V transposed, all bf16 (rl_qkv_post's native outputs). Keys j >= nkv, and j >
     lim[i] for query i when lim (nq int32) is given, are not visible. Returns out, (nq, ldo) bf16 with head h at
     columns (h0 + h) * 128 (allocated as (nq, heads * 128) if None); quantize_out rounds each 8-dim block to bfp16.
-    See rl_attention in include/rlbfp.h."""
+    With split (the default) the tasks left over after whole rounds of the GPU are split along the keys, with a
+    workspace from torch's allocator (rl_attention_ws); split=False runs every task whole (rl_attention).
+    See rl_attention and rl_attention_ws in include/rlbfp.h."""
     for t, n in ((q, "q"), (k, "k"), (vt, "vt")):
         _dev(t, n)
         if t.dtype != torch.bfloat16 or not t.is_contiguous():
@@ -320,6 +322,9 @@ def attention(q, k, vt, nkv=None, lim=None, out=None, h0=0, quantize_out=False):
         _dev(lim, "lim")
         if lim.dtype != torch.int32 or lim.numel() != nq or not lim.is_contiguous():
             raise ValueError("lim must be a contiguous int32 tensor of nq entries")
-    L.check(L.lib().rl_attention(_ptr(q), _ptr(k), _ptr(vt), heads, nq, nk, nk if nkv is None else nkv, _ptr(lim),
-                                 _ptr(out), out.stride(0), h0, 1 if quantize_out else 0, _stream(q)))
+    nbytes = L.lib().rl_attention_workspace_bytes(heads, nq, nk) if split else 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes > 0 else None
+    L.check(L.lib().rl_attention_ws(_ptr(q), _ptr(k), _ptr(vt), heads, nq, nk, nk if nkv is None else nkv, _ptr(lim),
+                                    _ptr(out), out.stride(0), h0, 1 if quantize_out else 0, _ptr(ws), max(nbytes, 0),
+                                    _stream(q)))
     return out

@@ -270,8 +270,9 @@ def graph_us(call, warm, per_graph, reps):
 
 def attn_bench(dev, heads=24, per_graph=10, reps=3):
     """Attention over the benchmark's M (4352 tokens, 24 heads of 128 = hidden 3072): Q (score scale folded in), K,
-    V^T bf16 in, bf16 O out (4 * heads * M^2 * 128 FLOP); HIP-graph replays. torch's bf16 scaled_dot_product_attention
-    of the same shape is timed beside it as a reference point."""
+    V^T bf16 in, bf16 O out (4 * heads * M^2 * 128 FLOP); HIP-graph replays. `us` is the default launch (the last
+    partial round split along the keys, with its combine launch); `whole_tasks_us` runs every task whole. torch's bf16
+    scaled_dot_product_attention of the same shape is timed beside it as a reference point."""
     import torch
 
     from rlbfp import ops
@@ -282,6 +283,7 @@ def attn_bench(dev, heads=24, per_graph=10, reps=3):
     vt = torch.randn((heads, 128, M), generator=g, device=dev).to(torch.bfloat16)
     out = torch.empty((M, heads * 128), dtype=torch.bfloat16, device=dev)
     us = graph_us(lambda i: ops.attention(q, k, vt, out=out), 3, per_graph, reps)
+    us_whole = graph_us(lambda i: ops.attention(q, k, vt, out=out, split=False), 3, per_graph, reps)
     flops = 4.0 * heads * M * M * 128
     qs, ks, vs = q.unsqueeze(0), k.unsqueeze(0), vt.transpose(1, 2).contiguous().unsqueeze(0)
     f = torch.nn.functional.scaled_dot_product_attention
@@ -297,7 +299,8 @@ def attn_bench(dev, heads=24, per_graph=10, reps=3):
     us_t = e0.elapsed_time(e1) * 1e3 / per_graph
     tf = flops / (us * 1e-6) / 1e12
     return {"shape": [heads, M, M, 128], "us": round(us, 2), "tflops": round(tf, 1),
-            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "torch_sdpa_us": round(us_t, 2),
+            "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "whole_tasks_us": round(us_whole, 2),
+            "torch_sdpa_us": round(us_t, 2),
             "torch_sdpa_tflops": round(flops / (us_t * 1e-6) / 1e12, 1)}
 
 

@@ -282,8 +282,9 @@ def attn_bench(dev, heads=24, per_graph=10, reps=3):
     k = torch.randn((heads, M, 128), generator=g, device=dev).to(torch.bfloat16)
     vt = torch.randn((heads, 128, M), generator=g, device=dev).to(torch.bfloat16)
     out = torch.empty((M, heads * 128), dtype=torch.bfloat16, device=dev)
-    us = graph_us(lambda i: ops.attention(q, k, vt, out=out), 3, per_graph, reps)
-    us_whole = graph_us(lambda i: ops.attention(q, k, vt, out=out, split=False), 3, per_graph, reps)
+    # 20 warm-up calls each: the clocks take a few milliseconds of this load to settle
+    us = graph_us(lambda i: ops.attention(q, k, vt, out=out), 20, per_graph, reps)
+    us_whole = graph_us(lambda i: ops.attention(q, k, vt, out=out, split=False), 20, per_graph, reps)
     flops = 4.0 * heads * M * M * 128
     qs, ks, vs = q.unsqueeze(0), k.unsqueeze(0), vt.transpose(1, 2).contiguous().unsqueeze(0)
     f = torch.nn.functional.scaled_dot_product_attention

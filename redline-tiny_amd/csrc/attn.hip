@@ -107,11 +107,13 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
   const int l16 = lane & 15, lg = lane >> 4;
   const int nqb = a.nq / kAtQ, nblk = a.nk / kAtKB;
 
-  // Work is the flattened (task, key block) space, task = (head, 128-query block) with a head's query blocks
-  // adjacent (K/V shared in L2). Workgroups below nfull take one whole task. The others split the tail tasks' key
-  // blocks into contiguous ranges of `per` blocks; a task cut by a range boundary leaves one partial per range in the
-  // workspace, merged by attn_combine_kernel.
-  const int bid = blockIdx.x;
+  // Work is the flattened (task, key block) space, task = (head, query block) with a head's query blocks adjacent.
+  // Workgroups below nfull take one whole task. The others split the tail tasks' key blocks into contiguous ranges
+  // of `per` blocks; a task cut by a range boundary leaves one partial per range in the workspace, merged by
+  // attn_combine_kernel. Workgroups are dispatched round robin over the 8 XCDs; xcd_remap gives each XCD a contiguous
+  // run of tasks (and of ranges), so a head's K and V^T are pulled into fewer of the XCDs' L2 caches.
+  const int bid = (int)blockIdx.x < a.nfull ? xcd_remap(blockIdx.x, a.nfull)
+                                            : a.nfull + xcd_remap(blockIdx.x - a.nfull, gridDim.x - a.nfull);
   const int ti = bid - a.nfull;  // tail range index (negative for a whole-task workgroup)
   const int f0 = ti < 0 ? bid * nblk : a.nfull * nblk + ti * a.per;
   const int f1 = ti < 0 ? f0 + nblk : min(f0 + a.per, a.ntask * nblk);

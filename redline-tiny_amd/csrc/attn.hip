@@ -5,15 +5,17 @@
 // step drive (redline/run_attn.py:67-82, redline/forward.py:247, :369-377). As there, Q carries the score scale
 // log2(e)/sqrt(128), so scores are in log2 units and the softmax is 2^(s - max) / sum (attn_bfp.cc:1-12).
 //
-// Workgroup = 4 waves x 32 queries of one head; key blocks of 64 are staged in LDS (double buffered) and read by all
-// four waves. Per wave and key block, with v_mfma_f32_16x16x32_bf16:
+// Workgroup = 4 or 8 waves x 32 queries of one head; key blocks of 64 are staged in LDS (double buffered) and read by
+// all the waves. Per wave and key block, with v_mfma_f32_16x16x32_bf16:
 //   S^T (64 keys x 32 queries) = K Q^T: K rows are the A operand, Q^T (kept in registers) the B operand, so each lane
 //     holds 16 keys of one query and the softmax statistics of a query live in one lane column;
 //   O^T (128 dims x 32 queries) += V^T P^T: P^T comes straight out of the S^T registers as the B operand (its 8 keys
 //     per lane are keys 4g..4g+3 and 16+4g..16+4g+3 of a 32-key step), and the V^T A operand is read from LDS with
 //     the same key order. V arrives transposed (rl_qkv_post's V^T output), so no transpose is needed anywhere.
-// K rows in LDS are 256 bytes with the 16-byte chunks XOR-swizzled by key & 15, V^T rows 128 bytes with the 8-byte
-// units swizzled by dim & 15, so that the 16 lanes of an operand read hit distinct banks.
+// K rows in LDS are 256 bytes with the 16-byte chunks XOR-swizzled by key & 15. V^T rows are 128 bytes in which each
+// 32-key step keeps the 4-key groups g and g + 4 side by side (16-byte chunk 4c + g of step c), so that one 16-byte
+// read is a whole A operand; those chunks are XOR-swizzled by ((dim >> 1) & 7) ^ (dim & 1). Either way the lanes of
+// an operand read (16 per pass) and of a staging store hit distinct banks.
 #include <math.h>
 
 #include <algorithm>
@@ -89,6 +91,9 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   const bf16x2 v = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, v);
 }
+
+// Swizzle of the 16-byte chunks of V^T row dim (only dim % 16 matters)
+__device__ __forceinline__ int vswz(int dim) { return ((dim >> 1) & 7) ^ (dim & 1); }
 
 // A partial result of a key range, for the combine pass: O^T unnormalised [queries][128 dims], then the running max
 // m (log2 units; -inf when no key of the range was visible) and the sum l of each query, all fp32.
@@ -179,13 +184,21 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
         *reinterpret_cast<u32x4*>(sk + key * 256 + ((ch ^ (key & 15)) << 4)) = rk[i];
       }
     };
+    // V^T row byte of 4-key group k (keys 4k..4k+3 of the block): step c = k / 8, group w = k % 8 -> 16-byte chunk
+    // 4c + w % 4, half w / 4. Chunks are XOR-swizzled by vswz(dim): a permutation of 0..7 over the 8 rows of either
+    // parity among 16 consecutive rows (16 lanes of an operand read hit distinct banks), and of opposite parity for
+    // rows d, d + 1 (the 16 lanes of an 8-byte staging store, two rows, hit distinct 8-byte slots)
+    auto vslot = [](int dim, int k) {
+      const int w = k & 7;
+      return dim * 128 + ((((k >> 3) * 4 + (w & 3)) ^ vswz(dim)) << 4) + ((w >> 2) << 3);
+    };
     auto store_v = [&](int buf) {
       uint8_t* sv = vbuf + buf * kAtK;
 #pragma unroll
       for (int i = 0; i < NI; i++) {
-        const int c = tid + kAtThreads * i, dim = c >> 3, u = 2 * (c & 7);
-        *reinterpret_cast<uint2*>(sv + dim * 128 + ((u ^ (dim & 15)) << 3)) = uint2{rv[i].x, rv[i].y};
-        *reinterpret_cast<uint2*>(sv + dim * 128 + (((u + 1) ^ (dim & 15)) << 3)) = uint2{rv[i].z, rv[i].w};
+        const int c = tid + kAtThreads * i, dim = c >> 3, k = 2 * (c & 7);
+        *reinterpret_cast<uint2*>(sv + vslot(dim, k)) = uint2{rv[i].x, rv[i].y};
+        *reinterpret_cast<uint2*>(sv + vslot(dim, k + 1)) = uint2{rv[i].z, rv[i].w};
       }
     };
 
@@ -194,11 +207,13 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
     f32x4 S[2][4];
     auto scores = [&](int r) {
       const uint8_t* sk = kbuf + (r & 1) * kAtK;
+      // the first product of each tile takes {-m, -m, -m, -m} as its accumulator input straight from one register
+      // group per set, so no tile is initialised with moves
+      f32x4 nb4[2];
 #pragma unroll
       for (int s = 0; s < 2; s++) {
         const float nb = m[s] == -INFINITY ? 0.f : -m[s];
-#pragma unroll
-        for (int g = 0; g < 4; g++) S[s][g] = f32x4{nb, nb, nb, nb};
+        nb4[s] = f32x4{nb, nb, nb, nb};
       }
 #pragma unroll
       for (int g = 0; g < 4; g++) {
@@ -207,7 +222,7 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
           const int key = 16 * g + l16, ch = 4 * st + lg;
           const bf16x8 kA = *reinterpret_cast<const bf16x8*>(sk + key * 256 + ((ch ^ l16) << 4));
 #pragma unroll
-          for (int s = 0; s < 2; s++) S[s][g] = mfma16(kA, qB[s][st], S[s][g]);
+          for (int s = 0; s < 2; s++) S[s][g] = mfma16(kA, qB[s][st], st == 0 ? nb4[s] : S[s][g]);
         }
       }
     };
@@ -240,6 +255,7 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
         alpha[s] = 1.f;
         rebased[s] = __any(need);
         if (rebased[s]) {  // wave-uniform branch, rare after the first block
+          asm volatile("" ::: "memory");  // a real branch: executing this body on every block costs ~20 VALU per set
           alpha[s] = __builtin_amdgcn_exp2f(-delta);
           m[s] = need ? (m[s] == -INFINITY ? mx : m[s] + mx) : m[s];
           lsum[s] *= alpha[s];
@@ -270,8 +286,8 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
       }
     };
 
-    // O^T += V^T P^T of the segment's block r: A = V^T rows 16 dg + l16, keys in the P^T order (8-byte units 8c + lg,
-    // 8c + 4 + lg)
+    // O^T += V^T P^T of the segment's block r: A = V^T rows 16 dg + l16, keys in the P^T order (4-key groups lg and
+    // lg + 4 of step c: one 16-byte chunk)
     auto pv = [&](int r, const u32x4 (&Pb)[2][2]) {
       const uint8_t* sv = vbuf + (r & 1) * kAtK;
 #pragma unroll
@@ -279,9 +295,7 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
         const uint8_t* row = sv + (16 * dg + l16) * 128;
 #pragma unroll
         for (int c = 0; c < 2; c++) {
-          const uint2 v0 = *reinterpret_cast<const uint2*>(row + (((8 * c + lg) ^ l16) << 3));
-          const uint2 v1 = *reinterpret_cast<const uint2*>(row + (((8 * c + 4 + lg) ^ l16) << 3));
-          const bf16x8 vA = __builtin_bit_cast(bf16x8, u32x4{v0.x, v0.y, v1.x, v1.y});
+          const bf16x8 vA = *reinterpret_cast<const bf16x8*>(row + (((4 * c + lg) ^ vswz(l16)) << 4));
 #pragma unroll
           for (int s = 0; s < 2; s++) O[s][dg] = mfma16(vA, __builtin_bit_cast(bf16x8, Pb[s][c]), O[s][dg]);
         }

@@ -16,6 +16,8 @@
 // 32-key step keeps the 4-key groups g and g + 4 side by side (16-byte chunk 4c + g of step c), so that one 16-byte
 // read is a whole A operand; those chunks are XOR-swizzled by ((dim >> 1) & 7) ^ (dim & 1). Either way the lanes of
 // an operand read (16 per pass) and of a staging store hit distinct banks.
+// Built with -fno-honor-nans (Makefile): the running maxes then skip NaN quieting; +-inf keep their meaning. NaN in
+// Q, K or V is outside the contract.
 #include <math.h>
 
 #include <algorithm>

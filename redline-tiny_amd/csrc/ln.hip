@@ -154,12 +154,13 @@ __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel
         float sf[8], xf[8];
         unpack8(*reinterpret_cast<const u32x4*>(prm + D + cb * 8), sf);
         unpack8(v[j], xf);
-        uint32_t u[8], b[8];
+        uint32_t u[8];
         int32_t q[8];
+        u32x4 bw;
 #pragma unroll
         for (int e = 0; e < 8; e++) u[e] = __float_as_uint((xf[e] - mean) * rstd * sf[e]);
-        const uint32_t E = encode_block(u, q, b);
-        if (a.a_deq) *reinterpret_cast<u32x4*>(a.a_deq + r * a.ld_a + cb * 8) = pack8(b);
+        const uint32_t E = encode_block(u, q, bw);
+        if (a.a_deq) *reinterpret_cast<u32x4*>(a.a_deq + r * a.ld_a + cb * 8) = bw;
         if (a.a_packed) {
           const int pos = a_lay ? (cb >> 3) * 128 + (cb & 7) * 16 + (lr >> 3) * 8 + (lr & 7) : lr * nbr + cb;
           uint8_t* p = stage + pos * kBlockBytes;

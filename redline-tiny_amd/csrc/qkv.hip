@@ -89,18 +89,17 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
                            __uint_as_float(cr.y << 16), __uint_as_float(cr.y & 0xFFFF0000u)};
       const float s4[4] = {__uint_as_float(sr.x << 16), __uint_as_float(sr.x & 0xFFFF0000u),
                            __uint_as_float(sr.y << 16), __uint_as_float(sr.y & 0xFFFF0000u)};
-      uint32_t u[8], b[8];
+      uint32_t u[8];
       int32_t q[8];
+      u32x4 bw;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const float ev = xf[2 * i] * inv * wf[2 * i], od = xf[2 * i + 1] * inv * wf[2 * i + 1];
         u[2 * i] = __float_as_uint(ev * c4[i] - od * s4[i]);
         u[2 * i + 1] = __float_as_uint(ev * s4[i] + od * c4[i]);
       }
-      const uint32_t E = encode_block(u, q, b);
-      if (nat)
-        *reinterpret_cast<u32x4*>(nat + (((int64_t)h * a.M + row) * kHeadDim + bc * 8)) =
-            u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+      const uint32_t E = encode_block(u, q, bw);
+      if (nat) *reinterpret_cast<u32x4*>(nat + (((int64_t)h * a.M + row) * kHeadDim + bc * 8)) = bw;
       // a_layout(64, 128) for Q and b_layout(K^T, 128, 64) for K order a tile's blocks the same way:
       // 16-token band, 8-dim block, 8-token half, token
       if (tiles) stage_block(stage, (((r >> 4) * 16 + bc) * 2 + ((r >> 3) & 1)) * 8 + (r & 7), E, q);
@@ -111,14 +110,14 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int item = tid + kQkvThreads * i, d = item & 127, kb = item >> 7;
-      uint32_t u[8], b[8];
+      uint32_t u[8];
       int32_t q[8];
+      u32x4 bw;
 #pragma unroll
       for (int e = 0; e < 8; e++) u[e] = (uint32_t)a.C[(row0 + kb * 8 + e) * a.ldc + col0 + d] << 16;
-      const uint32_t E = encode_block(u, q, b);
+      const uint32_t E = encode_block(u, q, bw);
       if (a.v)  // V^T: the block's 8 tokens are contiguous in row d
-        *reinterpret_cast<u32x4*>(a.v + ((int64_t)h * kHeadDim + d) * a.M + row0 + kb * 8) =
-            u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+        *reinterpret_cast<u32x4*>(a.v + ((int64_t)h * kHeadDim + d) * a.M + row0 + kb * 8) = bw;
       if (tiles) stage_block(stage, (((d >> 4) * 8 + kb) * 2 + ((d >> 3) & 1)) * 8 + (d & 7), E, q);
     }
   }

@@ -74,19 +74,15 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const void* __restr
       u[0] = a.x; u[1] = a.y; u[2] = a.z; u[3] = a.w; u[4] = b.x; u[5] = b.y; u[6] = b.z; u[7] = b.w;
     }
     int32_t q[8];
-    uint32_t b[8];
-    const uint32_t E = encode_block(u, q, b);
+    u32x4 bw;
+    const uint32_t E = encode_block(u, q, bw);
     if (packed) {
       uint8_t* s = stage + threadIdx.x * kBlockBytes;
       s[0] = (uint8_t)E;
 #pragma unroll
       for (int i = 0; i < 8; i++) s[1 + i] = (uint8_t)(int8_t)q[i];
     }
-    if (deq) {
-      u32x4 o;
-      o.x = b[0] | (b[1] << 16); o.y = b[2] | (b[3] << 16); o.z = b[4] | (b[5] << 16); o.w = b[6] | (b[7] << 16);
-      *reinterpret_cast<u32x4*>(deq + r * cols + cb * 8) = o;
-    }
+    if (deq) *reinterpret_cast<u32x4*>(deq + r * cols + cb * 8) = bw;
   }
   if (!packed) return;
   __syncthreads();

@@ -143,25 +143,61 @@ __device__ __forceinline__ u32x4 quantize_bf16x8(u32x4 v, uint32_t* E_out = null
   return r;
 }
 
-// Encode 8 float32 bit patterns (finite) to one block: returns E, writes q and the decoded values' bf16 bits.
-// For block exponents 7..254 the float path is used: powers of two scale exactly and v_rndne rounds half to even, so
-// it equals the integer encoder (scaled values too small to be normal round to 0 either way), and every decoded
-// value is a normal float. Other exponents take the integer encoder.
-__device__ __forceinline__ uint32_t encode_block(const uint32_t u[8], int32_t q[8], uint32_t b[8]) {
-  const uint32_t E = block_exp(u);
-  if (E >= 7u && E <= 254u) {
+// Float fast path of the encoder for a block exponent E in 7..237 (kFastEMin..kFastEMax). With s = 2^(133-E) and t = 127 * 2^(E-133):
+// fma(min(x, t), s, 1.5 * 2^23) scales exactly (a power of two) and rounds once, half to even, at integer
+// granularity, because the 1.5 * 2^23 term is even and |x * s| < 2^22. The result's bits are 0x4B400000 + q, so the
+// low byte is q in two's complement; min(x, t) clips q at 127, and q >= -128 holds by the choice of E. Values too small
+// to reach 0.5 after scaling round to 0, as the integer encoder gives. (f - 1.5 * 2^23) * 2^(E-133) is the decoded
+// value, exactly, and a normal float. Above E = 237 the constant -1.5 * 2^23 * 2^(E-133) of decode_fast overflows
+// float32, so such blocks (values of 2^111 and more) take the integer encoder.
+constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
+constexpr uint32_t kFastEMin = 7u, kFastEMax = 237u;
+struct BlockScale {
+  float s, t, inv;  // 2^(133-E), 127 * 2^(E-133), 2^(E-133)
+};
+__device__ __forceinline__ BlockScale block_scales(uint32_t E) {
+  return BlockScale{__uint_as_float((260u - E) << 23), __uint_as_float(0x42FE0000u + ((E - 133u) << 23)),
+                    __uint_as_float((E - 6u) << 23)};
+}
+__device__ __forceinline__ float encode_fast(float x, const BlockScale& k) {
+  return __builtin_fmaf(fminf(x, k.t), k.s, kMagic);
+}
+// Decoded value of an encode_fast result: f * 2^(E-133) is exact, and adding -1.5 * 2^23 * 2^(E-133) leaves
+// q * 2^(E-133), representable, so the fma does not round (+0 for q = 0)
+__device__ __forceinline__ float decode_fast(float f, const BlockScale& k, float off) { return __builtin_fmaf(f, k.inv, off); }
+__device__ __forceinline__ uint32_t decode_fast_bits(float f, const BlockScale& k) {
+  return __float_as_uint(decode_fast(f, k, -kMagic * k.inv)) >> 16;
+}
+
+// Encode 8 float32 bit patterns (finite) to one block: returns E, writes q (the int8 value in the low byte of each
+// word: callers store the byte) and the decoded values as bf16, packed two per word (value 2i in the low half of word
+// i). The largest exponent field is that of the largest magnitude. For block exponents 7..237 the float fast path
+// above is used; other exponents (subnormal blocks, very large ones, and infinities, which saturate) take the integer
+// encoder.
+__device__ __forceinline__ uint32_t encode_block(const uint32_t u[8], int32_t q[8], u32x4& bw) {
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(__uint_as_float(u[i])));
+  const uint32_t E = __float_as_uint(mx) >> 23;
+  if (E >= kFastEMin && E <= kFastEMax) {
+    const BlockScale k = block_scales(E);
+    const float off = -kMagic * k.inv;
+    float d[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float qf = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(__uint_as_float(u[i]), 133 - (int)E)), 127.0f);
-      q[i] = (int32_t)qf;
-      b[i] = __float_as_uint(__builtin_amdgcn_ldexpf(qf, (int)E - 133) + 0.0f) >> 16;  // exact in bf16; -0 -> +0
+      const float f = encode_fast(__uint_as_float(u[i]), k);
+      q[i] = (int32_t)__float_as_uint(f);
+      d[i] = decode_fast(f, k, off);
     }
+    bw = u32x4{pack_hi(d[0], d[1]), pack_hi(d[2], d[3]), pack_hi(d[4], d[5]), pack_hi(d[6], d[7])};
   } else {
+    uint32_t b[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       q[i] = encode_elem(u[i], E);
       b[i] = decode_bf16_bits(q[i], E);
     }
+    bw = u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
   }
   return E;
 }
@@ -169,9 +205,9 @@ __device__ __forceinline__ uint32_t encode_block(const uint32_t u[8], int32_t q[
 // One element quantized with a given block exponent E (the block's largest exponent field, found by the caller):
 // the bf16 bits of its bfp16 value. Same arithmetic as encode_block.
 __device__ __forceinline__ uint32_t quantize_with_exp(uint32_t u, uint32_t E) {
-  if (E >= 7u && E <= 254u) {
-    const float qf = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(__uint_as_float(u), 133 - (int)E)), 127.0f);
-    return __float_as_uint(__builtin_amdgcn_ldexpf(qf, (int)E - 133) + 0.0f) >> 16;
+  if (E >= kFastEMin && E <= kFastEMax) {
+    const BlockScale k = block_scales(E);
+    return decode_fast_bits(encode_fast(__uint_as_float(u), k), k);
   }
   return decode_bf16_bits(encode_elem(u, E), E);
 }

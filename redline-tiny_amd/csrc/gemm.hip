@@ -95,27 +95,24 @@ __device__ __forceinline__ uint32_t bf16_rne(float v) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-// Re-quantize one block of 8 bf16 values (4 packed words) to bfp16, returned as bf16 words. The scaling is by
-// powers of two (v_ldexp) and the rounding is v_rndne (half to even), so the result equals the integer encoder's;
-// blocks whose exponent is below 7 (values and steps in the float32 subnormal range) take the integer path so that
-// the result does not depend on the denormal mode. -0 comes back as +0, as from_bfp16 gives it.
+// Re-quantize one block of 8 bf16 values (4 packed words) to bfp16, returned as bf16 words: the encoder's float fast
+// path (encode_fast / decode_fast: one exact power-of-two scaling and one half-to-even rounding per value) for block
+// exponents 7..237, the integer encoder otherwise, so the result equals the integer encoder's and does not depend on
+// the denormal mode. -0 comes back as +0, as from_bfp16 gives it.
 __device__ __forceinline__ u32x4 requantize8(u32x4 o) {
   const uint32_t w[4] = {o.x, o.y, o.z, o.w};
   uint32_t E = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) E = max(E, max((w[k] >> 7) & 0xFFu, (w[k] >> 23) & 0xFFu));
-  if (E < 7u) return quantize_bf16x8(o);
+  if (E < kFastEMin || E > kFastEMax) return quantize_bf16x8(o);
+  const BlockScale sc = block_scales(E);
+  const float off = -kMagic * sc.inv;
   uint32_t r[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    float v[2] = {__uint_as_float(w[k] << 16), __uint_as_float(w[k] & 0xFFFF0000u)};
-    uint32_t b[2];
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-      const float q = fminf(__builtin_rintf(__builtin_amdgcn_ldexpf(v[t], 133 - (int)E)), 127.0f);
-      b[t] = __float_as_uint(__builtin_amdgcn_ldexpf(q, (int)E - 133) + 0.0f) >> 16;
-    }
-    r[k] = b[0] | (b[1] << 16);
+    const float lo = decode_fast(encode_fast(__uint_as_float(w[k] << 16), sc), sc, off);
+    const float hi = decode_fast(encode_fast(__uint_as_float(w[k] & 0xFFFF0000u), sc), sc, off);
+    r[k] = pack_hi(lo, hi);
   }
   return u32x4{r[0], r[1], r[2], r[3]};
 }

@@ -14,7 +14,7 @@
 
 namespace rl {
 
-constexpr int kVWaves = 2;                    // waves per workgroup; they split K
+constexpr int kVWaves = 3;                    // waves per workgroup; they split K
 constexpr int kVThreads = 64 * kVWaves;
 constexpr int kVIterBytes = 8 * 1152;         // one wave iteration: 8 K tiles of one 16-column group = 9 x 1 KB
 
@@ -22,22 +22,24 @@ __device__ __forceinline__ float silu_v(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
 
-// Workgroup = one 16-column group g of the b_layout (N tile g / 8, super-block g % 8), all of K. Wave w takes the
-// iterations it = w, w + 2, ... of 8 K tiles each. An iteration's 8 x 1152 bytes are read with 9 coalesced 1 KB
+// Workgroup = one 16-column group g of the b_layout (N tile g / 8, super-block g % 8), all of K. Wave w of 3 takes
+// the iterations it = w, w + 3, ... of 8 K tiles each (2 per wave at K = 3072: 3456 waves, at most 4 per SIMD, all
+// resident with 112 VGPRs). An iteration's 8 x 1152 bytes are read with 9 coalesced 1 KB
 // loads; they pass through the wave's own 9 KB of LDS, from which lane l = (run, br) = (l/8, l%8) reads its 16 blocks
 // (K rows br*8..+7 of K tile 8 it + run, 16 columns) as 144 aligned bytes at offset 144 l (a 36-dword stride, which
-// covers all banks). Iterations go in groups of three whose loads are all issued at once (the first straight into
-// LDS, the other two into registers), which is all of a wave's 27 KB at K = 3072, and act(x) for the three is
-// quantized while the blocks are in flight: the math left behind the last bytes to arrive is the block products.
+// covers all banks). Iterations go in groups of two whose loads are issued at once (the first straight into LDS, the
+// other into registers), which is all of a wave's 18 KB at K = 3072, and act(x) for both is quantized while the
+// blocks are in flight: the math left behind the last bytes to arrive is the block products of at most two
+// iterations. (Two waves of three iterations each took 5% longer: more math behind the last bytes per wave.)
 //
 // act(x) of the lane's 8 K rows is quantized to one bfp16 block per row of x (E = largest float32 exponent field,
 // q = rint(v * 2^(133-E)) clipped to [-128, 127], as the activation encoder does), so that each weight block
 // contributes 2^(Ew + Ex - 266) * (qw . qx) with two 4-way int8 dot products, exactly in int32.
 template <int M, bool SILU>
-__global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv_kernel(
+__global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ B, uint16_t* __restrict__ y,
     int64_t ldy, int32_t N, int32_t K) {
-  constexpr int S = 2;  // register slots: one iteration in flight while the other is used
+  constexpr int S = 1;  // register slots: with the LDS slot, a group of two iterations in flight
   __shared__ __attribute__((aligned(16))) uint8_t buf[kVWaves][kVIterBytes];
   __shared__ float red[kVWaves][M][16];
   // the wave index is uniform across the wave: readfirstlane puts it (and the load offsets built from it) in scalar
@@ -148,13 +150,13 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv
     }
   };
 
-  // Iterations go in groups of three, all requested at once: the first into LDS, the other two into the register
+  // Iterations go in groups of 1 + S, all requested at once: the first into LDS, the others into the register
   // slots. A group is straight-line code, so each wait is for its own iteration only (with uses under a branch the
   // compiler would sink the loads into it). Loads past this wave's iterations are safe: buffer loads beyond the
   // stream return zeros, x loads use a clamped K tile.
   for (int g0 = 0; g0 < mine; g0 += 1 + S) {
-    // issue order (fenced, and the waits below count on it): the three iterations' x rows, then the blocks of
-    // the first (into LDS), the second and the third
+    // issue order (fenced, and the waits below count on it): the group's x rows, then the blocks of the first
+    // iteration (into LDS), then those of the others
     xload(g0, x0);
 #pragma unroll
     for (int s0 = 0; s0 < S; s0++) xload(g0 + 1 + s0, xs[s0]);
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 3 : (M <= 3 ? 2 : 1)) void gemv
       wload(g0 + 1 + s0, w[s0]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // the x rows land first: for up to 4 rows of x, act(x) of all three iterations is quantized while the blocks
+    // the x rows land first: for up to 4 rows of x, act(x) of all the group's iterations is quantized while the blocks
     // are still in flight (more rows would not fit the registers; they are quantized per iteration)
     constexpr bool kEarly = M <= 4;
     XQ xq[1 + S];

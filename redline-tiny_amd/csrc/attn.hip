@@ -151,6 +151,9 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int dg = 0; dg < 8; dg++) O[s][dg] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+    // {-m, -m, -m, -m} per set (0 while no key has been visible), the first score product's accumulator input;
+    // changed only when the running max is rebased
+    f32x4 nb4[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 
     // LDS: K buffers 0, 1, then V^T buffers 0, 1 (16 KB each). K runs one key block ahead of V: iteration j computes
     // S(j + 1) from K buffer (j + 1) % 2 while O accumulates P(j) V(j) from V buffer j % 2, and the softmax of block
@@ -211,12 +214,6 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
       const uint8_t* sk = kbuf + (r & 1) * kAtK;
       // the first product of each tile takes {-m, -m, -m, -m} as its accumulator input straight from one register
       // group per set, so no tile is initialised with moves
-      f32x4 nb4[2];
-#pragma unroll
-      for (int s = 0; s < 2; s++) {
-        const float nb = m[s] == -INFINITY ? 0.f : -m[s];
-        nb4[s] = f32x4{nb, nb, nb, nb};
-      }
 #pragma unroll
       for (int g = 0; g < 4; g++) {
 #pragma unroll
@@ -260,6 +257,8 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
           asm volatile("" ::: "memory");  // a real branch: executing this body on every block costs ~20 VALU per set
           alpha[s] = __builtin_amdgcn_exp2f(-delta);
           m[s] = need ? (m[s] == -INFINITY ? mx : m[s] + mx) : m[s];
+          const float nb = m[s] == -INFINITY ? 0.f : -m[s];
+          nb4[s] = f32x4{nb, nb, nb, nb};
           lsum[s] *= alpha[s];
 #pragma unroll
           for (int g = 0; g < 4; g++)
@@ -318,12 +317,13 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
     scores(0);
     softmax(kb0, Pb, alpha, rebased);  // O is still 0: no rescale
     // Every load and store below is unconditional: past the last block they repeat block kb1 - 1 into a buffer that is
-    // not read again, which keeps the loop free of branches around memory operations.
-    for (int j = 0; j + 1 < nb; j++) {
+    // not read again, which keeps the loop free of branches around memory operations. The loop runs two blocks per
+    // trip, so each buffer index is a constant (an immediate LDS offset, no address arithmetic per block).
+    auto iter = [&]<int P>(int j) {  // P = j % 2
       load_v(kb0 + j + 1);
       load_k(kb0 + min(j + 2, nb - 1));
-      scores(j + 1);
-      pv(j, Pb);
+      scores(1 - P);
+      pv(P, Pb);
       u32x4 Pn[2][2];
       softmax(kb0 + j + 1, Pn, alpha, rebased);
 #pragma unroll
@@ -335,11 +335,21 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int c = 0; c < 2; c++) Pb[s][c] = Pn[s][c];
       }
-      store_v((j + 1) & 1);  // V buffer (j + 1) % 2 held V(j - 1), read in iteration j - 1
-      store_k(j & 1);        // K buffer j % 2 held K(j), read in iteration j - 1
+      store_v(1 - P);  // V buffer (j + 1) % 2 held V(j - 1), read in iteration j - 1
+      store_k(P);      // K buffer j % 2 held K(j), read in iteration j - 1
       __syncthreads();
+    };
+    int j = 0;
+    for (; j + 2 < nb; j += 2) {
+      iter.template operator()<0>(j);
+      iter.template operator()<1>(j + 1);
     }
-    pv(nb - 1, Pb);
+    if (j + 1 < nb) {
+      iter.template operator()<0>(j);
+      pv(1, Pb);  // block nb - 1 = j + 1 is odd
+    } else {
+      pv(0, Pb);  // block nb - 1 = j is even
+    }
 
     if (kb0 > 0 || kb1 < nblk) {
       // a piece of a task: O^T, m and l unnormalised into the workspace slot (tail task, piece)

@@ -49,10 +49,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// float -> bf16 bits, round to nearest even (finite inputs)
-__device__ __forceinline__ uint32_t bf16_rne(float f) {
-  const uint32_t u = __float_as_uint(f);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats -> one word of two bf16, each rounded to nearest even (one v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ void unpack8(u32x4 v, float f[8]) {
@@ -62,9 +64,6 @@ __device__ __forceinline__ void unpack8(u32x4 v, float f[8]) {
   f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
 }
 
-__device__ __forceinline__ u32x4 pack8(const uint32_t b[8]) {
-  return u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
-}
 
 // Template NB = blocks of 8 per lane (D / 512 rounded up); lanes whose block lies past the row end hold zeros and
 // skip every access. The register budget per NB is the smallest that compiles without spills; for D = 3072 (NB 6)
@@ -118,13 +117,17 @@ __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel
 #pragma unroll
           for (int e = 0; e < 8; e++) bf[e] = __builtin_amdgcn_ldexpf((float)q[e], sh);  // exact, as from_bfp16
         }
-        uint32_t xb[8];
+        // g * branch is exact in fp32: one rounding in the fma, then RNE to bf16; the mean's sum takes the bf16 pairs
+        // with one dot2 against (1, 1)
+        uint32_t xw[4];
+        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          xb[e] = bf16_rne(fmaf(gf[e], bf[e], xf[e]));  // g * branch is exact in fp32: one rounding, then RNE
-          s += __uint_as_float(xb[e] << 16);
+        for (int e = 0; e < 4; e++) {
+          const int i = 2 * e;
+          xw[e] = pack_bf16_rne(fmaf(gf[i], bf[i], xf[i]), fmaf(gf[i + 1], bf[i + 1], xf[i + 1]));
+          s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[e]), one, s, false);
         }
-        v[j] = pack8(xb);
+        v[j] = u32x4{xw[0], xw[1], xw[2], xw[3]};
         if (a.x_out) *reinterpret_cast<u32x4*>(a.x_out + r * a.ld_xo + cb * 8) = v[j];
       }
     }

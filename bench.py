@@ -14,7 +14,9 @@ launch stream.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
 rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
 produces the up GEMM's A (4352 x 3072) and the QKV post pass (4352 tokens x 24 heads) in GB/s against HBM; attention
-over 4352 tokens x 24 heads in TFLOP/s (torch's SDPA beside it); and the CPU baseline (the oracle's numpy restatement of the reference CPU path on a row sample of the same workload).
+over 4352 tokens x 24 heads in TFLOP/s (torch's SDPA beside it); the GEMMs of the other reference configurations
+(1, 2, 4 and 5: see configs_bench) in TFLOP/s; and the CPU baseline (the oracle's numpy restatement of the reference
+CPU path on a row sample of the same workload).
 
 Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--copy-probe MB] [--sustain SECONDS]
 """
@@ -197,6 +199,7 @@ def gpu_bench(steps, warmup):
         "ln": ln_bench(dev),
         "qkv": qkv_bench(dev),
         "attn": attn_bench(dev),
+        "configs": configs_bench(dev),
     }
 
 
@@ -303,6 +306,77 @@ def attn_bench(dev, heads=24, per_graph=10, reps=3):
             "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4), "whole_tasks_us": round(us_whole, 2),
             "torch_sdpa_us": round(us_t, 2),
             "torch_sdpa_tflops": round(flops / (us_t * 1e-6) / 1e12, 1)}
+
+
+def configs_bench(dev, per_graph=10, reps=3):
+    """The other reference configurations' GEMMs, timed like the FFN pair (HIP-graph replays, A already quantized
+    along K): config 1 (4096 x 3072 x 3072, no epilogue), config 2 (QKV 4352 x 3072 x 9216 with bias and 1% outlier
+    channels), config 4 (text-encoder MLP, M = 512: up K = 4096, N = 2 x 12288 SwiGLU re-quantized, down K = 12288,
+    N = 4096) and config 5 (one DiT block's GEMMs for the image (M = 4096) and text (M = 256) streams with separate
+    weights: QKV, out-projection, SwiGLU up and down, each op one grouped launch of both streams). Synthetic data of
+    those shapes; weights ~N(0, 0.02) packed on the GPU. FLOP = 2 M N K, N counting both SwiGLU halves."""
+    import torch
+
+    from rlbfp import ops
+
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def act(M, K, outliers=0.0):
+        a = torch.randn((M, K), generator=g, device=dev)
+        if outliers:
+            idx = torch.randperm(K, generator=g, device=dev)[: round(outliers * K)]
+            a[:, idx] *= 20
+        return ops.quantize(a.to(torch.bfloat16), deq=True)[1]
+
+    def weight(N, K):
+        return ops.pack_weight(torch.randn((N, K), generator=g, device=dev) * 0.02)
+
+    def up_weight(F_, K):
+        return ops.pack_weight(ops.interleave_up(torch.randn((F_, K), generator=g, device=dev) * 0.02,
+                                                 torch.randn((F_, K), generator=g, device=dev) * 0.02))
+
+    def line(us, flop):
+        tf = flop / (us * 1e-6) / 1e12
+        return {"us": round(us, 2), "tflops": round(tf, 1), "frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                "gflop": round(flop / 1e9, 2)}
+
+    out = {}
+    a1, w1 = act(4096, 3072), weight(3072, 3072)
+    c1 = torch.empty((4096, 3072), dtype=torch.bfloat16, device=dev)
+    out["cfg1"] = line(graph_us(lambda i: ops.gemm(a1, w1, 3072, 3072, out=c1), 5, per_graph, reps),
+                       2.0 * 4096 * 3072 * 3072)
+    a2, w2 = act(4352, 3072, outliers=0.01), weight(9216, 3072)
+    b2 = torch.randn(9216, generator=g, device=dev) * 0.02
+    c2 = torch.empty((4352, 9216), dtype=torch.bfloat16, device=dev)
+    out["cfg2"] = line(graph_us(lambda i: ops.gemm(a2, w2, 9216, 3072, bias=b2, out=c2), 5, per_graph, reps),
+                       2.0 * 4352 * 3072 * 9216)
+    x4 = act(512, 4096)
+    up4, dn4 = up_weight(12288, 4096), weight(4096, 12288)
+    h4 = torch.empty((512, 12288), dtype=torch.bfloat16, device=dev)
+    y4 = torch.empty((512, 4096), dtype=torch.bfloat16, device=dev)
+
+    def cfg4(i):
+        ops.gemm(x4, up4, 2 * 12288, 4096, act="swiglu", quantize_out=True, out=h4)
+        ops.gemm(h4, dn4, 4096, 12288, out=y4)
+
+    out["cfg4"] = line(graph_us(cfg4, 5, per_graph, reps), 2.0 * 512 * 4096 * 24576 + 2.0 * 512 * 12288 * 4096)
+    # config 5: per stream the four ops' inputs and weights (the ops are not chained here: timing only)
+    K = 3072
+    ops5 = []
+    for N, Kop, kind in ((9216, K, None), (K, K, None), (2 * 12288, K, "swiglu"), (K, 12288, None)):
+        specs = []
+        for M in (4096, 256):
+            a = act(M, Kop)
+            w = up_weight(12288, Kop) if kind == "swiglu" else weight(N, Kop)
+            specs.append(ops.GemmSpec(a, w, N, Kop, act=kind, quantize_out=kind == "swiglu"))
+        ops5.append(specs)
+
+    def cfg5(i):
+        for specs in ops5:
+            ops.gemm_grouped(specs)
+
+    out["cfg5"] = line(graph_us(cfg5, 5, per_graph, reps), 2.0 * 4352 * K * (9216 + K + 2 * 12288 + 12288))
+    return out
 
 
 def qkv_bench(dev, heads=24, sets=3, per_graph=30, reps=4):
@@ -525,6 +599,7 @@ def main():
         "ln_modulate": r["ln"],
         "qkv_post": r["qkv"],
         "attention": r["attn"],
+        "configs": r["configs"],
     }
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(r["host"], r["p_up"], r["p_down"])
     print(json.dumps(line), flush=True)

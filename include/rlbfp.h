@@ -100,6 +100,20 @@ typedef struct rl_epilogue {
 int rl_bfp16_gemm(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
                   int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *stream);
 
+/* rl_bfp16_gemm with a caller's workspace (device memory, 16-byte aligned), which lets a GEMM whose output tiles fill
+ * few compute units (small M, deep K: the text encoder's down projection at M = 512, K = 12288) split K into pieces
+ * that run side by side. Each piece writes fp32 partial sums to the workspace; a second launch adds them in piece
+ * order and applies the epilogue as above (results differ from the whole-K sums by fp32 rounding only). Only
+ * RL_A_BF16 splits. workspace NULL, or a shape the planner keeps whole: exactly rl_bfp16_gemm. workspace_bytes below
+ * rl_bfp16_gemm_workspace_bytes(): RL_ERR_WORKSPACE. Calls that share a workspace on different streams race. Same
+ * reference interface as rl_bfp16_gemm (redline/forward.py:194-197). */
+int rl_bfp16_gemm_ws(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *workspace, int64_t workspace_bytes,
+                     void *stream);
+/* Workspace bytes rl_bfp16_gemm_ws needs for an RL_A_BF16 GEMM of this shape on the current device (0: this shape
+ * runs whole; -1: the shape is invalid). */
+int64_t rl_bfp16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
 /* Several independent GEMMs (different shapes, weights and epilogues, one A format) in one launch, e.g. the image-
  * and text-stream projections of a DiT block. At most RL_MAX_GROUP descriptors. Replaces the per-op sequence of
  * CachedStep.blocks (redline/forward.py:240-254) for GEMMs that do not depend on each other. */

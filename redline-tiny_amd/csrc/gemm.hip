@@ -45,7 +45,9 @@ struct GemmDesc {
   const float* gate;
   const uint16_t* res;
   int64_t ldr;
-  int32_t tiles_m, tiles_n, tile_start, pad_;
+  int32_t tiles_m, tiles_n, tile_start;
+  int32_t ksplit;  // K pieces (8-wave kernel): 1 = whole K; > 1 = each piece writes fp32 partials to `part`
+  float* part;     // [ksplit][M][N] fp32 partial sums of the pieces, summed by gemm_reduce_kernel
 };
 
 template <int G>
@@ -244,6 +246,67 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
   }
 }
 
+// The K-piece variant of ep8_finish: the LDS tile holds raw fp32 sums of `nquads` row quads x 256 computed columns
+// (staged column c is column c0 + c); each thread stores blocks of 4 rows x 8 columns to plane `piece` of d.part.
+__device__ __forceinline__ void ep8_partial(const GemmDesc& d, const float* ep, int r0, int c0, int nquads, int piece,
+                                           int tid) {
+  for (int it = tid; it < nquads * 32; it += kG8ThreadsDecl) {
+    const int q = it >> 5, cb = it & 31;
+    const int col = c0 + 8 * cb;
+    if (col >= d.N) continue;
+    f32x4 a[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * 256 + ep_slot(8 * cb + k)) * 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * q + i;
+      if (row >= d.M) break;
+      float* dst = d.part + ((int64_t)piece * d.M + row) * d.N + col;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{a[0][i], a[1][i], a[2][i], a[3][i]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{a[4][i], a[5][i], a[6][i], a[7][i]};
+    }
+  }
+}
+
+// Sum of the K pieces' partials of a split GEMM, in piece order, then the epilogue: bias, activation (for SwiGLU
+// silu(gate) * proj of the output block's gate and proj columns), gate / residual, bf16 rounding and the optional
+// re-quantize, as the whole-K kernel applies them. One thread per output block of 8 columns.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmDesc d) {
+  const bool swiglu = d.act == RL_ACT_SWIGLU;
+  const int nout = swiglu ? d.N / 2 : d.N;
+  const int nb = nout / 8;
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (b >= (int64_t)d.M * nb) return;
+  const int row = (int)(b / nb), ocol = 8 * (int)(b % nb);
+  const int64_t plane = (int64_t)d.M * d.N;
+  const float* p = d.part + (int64_t)row * d.N;
+  // computed columns of the block: ocol itself, or the gate columns 128 t + u and proj columns 128 t + 64 + u
+  const int c0 = swiglu ? 128 * (ocol >> 6) + (ocol & 63) : ocol;
+  float s0[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, s1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < d.ksplit; k++) {
+    const float* q = p + k * plane + c0;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(q), a2 = *reinterpret_cast<const f32x4*>(q + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) { s0[e] += a[e]; s0[4 + e] += a2[e]; }
+    if (swiglu) {
+      const f32x4 g = *reinterpret_cast<const f32x4*>(q + 64), g2 = *reinterpret_cast<const f32x4*>(q + 68);
+#pragma unroll
+      for (int e = 0; e < 4; e++) { s1[e] += g[e]; s1[4 + e] += g2[e]; }
+    }
+  }
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = s0[e] + (d.bias ? d.bias[c0 + e] : 0.f);
+    if (swiglu)
+      v[e] = silu_f(x) * (s1[e] + (d.bias ? d.bias[c0 + 64 + e] : 0.f));
+    else
+      v[e] = d.act == RL_ACT_GELU_TANH ? gelu_tanh_f(x) : x;
+  }
+  const u32x4 o = finish_block(d, row, ocol, nout, v);
+  *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
+}
+
 // Loads this thread's eight 16-byte A chunks of K step kt: rows (tid>>3) + 32i, chunk tid&7.
 template <int AFMT>
 __device__ __forceinline__ void load_a(const GemmDesc& d, int m0, int kt, int tid, u32x4 (&av)[8]) {
@@ -298,7 +361,14 @@ __global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> ar
       if (pid >= args.d[i].tile_start) di = i;
   }
   const GemmDesc& d = args.d[di];
-  const int local = pid - d.tile_start;
+  int local = pid - d.tile_start;
+  // K pieces: piece p covers K steps [p KT / ksplit, (p + 1) KT / ksplit) of every tile; tiles of one piece are
+  // consecutive in launch order
+  int piece = 0;
+  if (d.ksplit > 1) {
+    piece = local / (d.tiles_m * d.tiles_n);
+    local -= piece * d.tiles_m * d.tiles_n;
+  }
   const int group = local / (kGroupM * d.tiles_n);
   const int first_m = group * kGroupM;
   const int gm = min(d.tiles_m - first_m, kGroupM);
@@ -585,7 +655,14 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
       if (pid >= args.d[i].tile_start) di = i;
   }
   const GemmDesc& d = args.d[di];
-  const int local = pid - d.tile_start;
+  int local = pid - d.tile_start;
+  // K pieces: piece p covers K steps [p KT / ksplit, (p + 1) KT / ksplit) of every tile; tiles of one piece are
+  // consecutive in launch order
+  int piece = 0;
+  if (d.ksplit > 1) {
+    piece = local / (d.tiles_m * d.tiles_n);
+    local -= piece * d.tiles_m * d.tiles_n;
+  }
   const int group = local / (kGroupM * d.tiles_n);
   const int first_m = group * kGroupM;
   const int gm = min(d.tiles_m - first_m, kGroupM);
@@ -595,7 +672,9 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
-  const int KT = d.K / BK;
+  const int KTt = d.K / BK;                    // K steps of the whole product (the b_layout tile stride)
+  const int kb = piece * KTt / d.ksplit;        // this piece's first K step
+  const int KT = (piece + 1) * KTt / d.ksplit - kb;
   const int N = d.N;
   const bool swiglu = d.act == RL_ACT_SWIGLU;
 
@@ -622,7 +701,8 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   // check) when it lies beyond N; its decode is never read.
   const int64_t nt0 = n0 >> 7;
   const int bh = tid >> 8, bu = tid & 255;
-  const uint32_t vb = nt0 + bh < (N >> 7) ? (uint32_t)((nt0 + bh) * KT * kTileBytes + 36 * bu) : 0x7FFFFFF0u;
+  const uint32_t vb =
+      nt0 + bh < (N >> 7) ? (uint32_t)(((nt0 + bh) * KTt + kb) * kTileBytes + 36 * bu) : 0x7FFFFFF0u;
   // group G = 8 h + c goes to LDS slot 4 (2 h + c / 2 % 2) + 2 (c / 4) + c % 2. Inside a 1 KB fragment, block m sits
   // at position frag_pos(m) (a 4 x 4 transpose in each 16 blocks, bit 2 flipped in odd 16s), not m: measured on
   // gfx950, this keeps both the operand reads (lane m reads block m) and the decode stores (store J: lane a writes
@@ -669,8 +749,10 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   // the buffer resource and read zeros.
   const int g0 = min(kDma * wave, TM / 8 - kDma);
   const int ar0 = 8 * g0 + (lane >> 3);
-  const uint32_t va_e = (uint32_t)(((int64_t)(m0 + ar0) * d.lda + ((lane & 7) ^ a_swz(ar0)) * 8) * 2);
-  const uint32_t va_o = (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + ((lane & 7) ^ a_swz(ar0 + 8)) * 8) * 2);
+  const uint32_t va_e =
+      (uint32_t)(((int64_t)(m0 + ar0) * d.lda + (int64_t)kb * BK + ((lane & 7) ^ a_swz(ar0)) * 8) * 2);
+  const uint32_t va_o =
+      (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + (int64_t)kb * BK + ((lane & 7) ^ a_swz(ar0 + 8)) * 8) * 2);
   const uint32_t va_16 = (uint32_t)(16 * d.lda * 2);
   auto dma_a = [&](int stage, int k, int i) {
     uint32_t v = (i & 1) ? va_o : va_e;
@@ -791,6 +873,26 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   // other activations TM / 2 rows x 256 columns per pass.
   float* ep = reinterpret_cast<float*>(lds);
   const int col_in = lane & 15;
+  if (d.ksplit > 1) {
+    // a K piece: the raw fp32 sums (no bias, activation or SwiGLU product) of TM / 2 rows x 256 columns per pass,
+    // staged like the plain epilogue, then stored to the piece's partial plane
+#pragma unroll
+    for (int P = 0; P < 2; P++) {
+      if (active && wm == P) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int c = ep_slot(16 * grp[j] + col_in);
+#pragma unroll
+          for (int mf = 0; mf < MF; mf++)
+            *reinterpret_cast<f32x4*>(ep + ((4 * mf + (lane >> 4)) * 256 + c) * 4) = acc[mf][j];
+        }
+      }
+      __syncthreads();
+      ep8_partial(d, ep, m0 + TM / 2 * P, n0, TM / 8, piece, tid);
+      __syncthreads();
+    }
+    return;
+  }
   const int nout = swiglu ? N / 2 : N;
   float bj[4];
 #pragma unroll
@@ -868,7 +970,8 @@ static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, 
   g.tiles_m = (int32_t)((M + BM - 1) / BM);
   g.tiles_n = (int32_t)((N + BN - 1) / BN);
   g.tile_start = tile_start;
-  g.pad_ = 0;
+  g.ksplit = 1;
+  g.part = nullptr;
   return RL_OK;
 }
 
@@ -908,6 +1011,45 @@ static Plan8 plan8(int64_t M, int64_t N, int cus) {
   return best;
 }
 
+// ---- K split (one GEMM whose tiles fill few CUs: small M, deep K) ------------------------------------------------
+// Model, in microseconds at the running clock: a tile of MF fragments costs kStepUs (MF + 1) per K step plus kTileUs
+// (prologue and epilogue), and a launch of T tiles takes ceil(T / CUs) such rounds. The reduce launch reads the
+// ksplit fp32 planes of M x N and writes the output: kReduceUs + bytes / kReduceBw. A split, with every piece in one
+// round, is taken when the model puts it under 3/4 of the best whole-K launch.
+constexpr double kStepUs = 0.18, kTileUs = 3.0, kReduceUs = 2.0, kReduceBw = 4.0e6;  // kReduceBw: bytes per us
+constexpr int kMaxSplit = 16, kMinPieceSteps = 8;
+constexpr int64_t kMaxSplitBytes = int64_t(1) << 30;
+
+struct SplitPlan {
+  int mf;            // fragments per wave
+  int ks;            // K pieces; 1 = no split
+  int64_t ws_bytes;  // fp32 partial planes: ks * M * N * 4
+};
+
+static SplitPlan plan_split(int64_t M, int64_t N, int64_t K, int cus) {
+  SplitPlan best{8, 1, 0};
+  if (cus <= 0) return best;
+  const int64_t KT = K / BK;
+  auto tile_us = [](int mf, int64_t steps) { return (double)steps * (mf + 1) * kStepUs + kTileUs; };
+  double whole = 1e300;
+  for (int mf : kMfChoices) {
+    const int64_t t = tiles8(M, N, mf);
+    const double c = (double)((t + cus - 1) / cus) * tile_us(mf, KT);
+    if (c < whole) whole = c;
+  }
+  double bc = 0.75 * whole;
+  for (int mf : kMfChoices) {
+    const int64_t t = tiles8(M, N, mf);
+    for (int ks = 2; ks <= kMaxSplit && t * ks <= cus && KT / ks >= kMinPieceSteps; ks++) {
+      const int64_t bytes = (int64_t)ks * M * N * 4;
+      if (bytes > kMaxSplitBytes) break;
+      const double c = tile_us(mf, (KT + ks - 1) / ks) + kReduceUs + (double)(bytes + M * N) / kReduceBw;
+      if (c < bc) { bc = c; best = SplitPlan{mf, ks, bytes}; }
+    }
+  }
+  return best;
+}
+
 template <int G>
 static void set_tiles8(GemmArgs<G>& args, int mf, int& total) {
   total = 0;
@@ -915,7 +1057,7 @@ static void set_tiles8(GemmArgs<G>& args, int mf, int& total) {
     GemmDesc& g = args.d[i];
     g.tiles_m = (int32_t)((g.M + 32 * mf - 1) / (32 * mf));
     g.tile_start = total;
-    total += g.tiles_m * g.tiles_n;
+    total += g.tiles_m * g.tiles_n * g.ksplit;
   }
   for (int i = args.n; i < G; i++) args.d[i] = args.d[args.n - 1];
 }
@@ -962,17 +1104,43 @@ static int launch(const GemmArgs<G>& args, int total_tiles, int32_t a_fmt, void*
 
 extern "C" {
 
-int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
-                  int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* stream) {
+int64_t rl_bfp16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  using namespace rl;
+  if (rl_validate_gemm(RL_A_BF16, K, N, M, N, K, nullptr)) return -1;
+  check_device();  // fills the compute-unit count when a device is present; 256 otherwise
+  ok();
+  return plan_split(M, N, K, device_cus()).ws_bytes;
+}
+
+int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* workspace, int64_t workspace_bytes,
+                     void* stream) {
   using namespace rl;
   GemmArgs<1> args;
   int s = fill_desc<1>(args.d[0], A, lda, B_packed, C, ldc, M, N, K, ep, a_fmt, 0);
   if (s) return s;
+  if ((uintptr_t)workspace % 16) return fail(RL_ERR_ALIGN, "the workspace must be 16-byte aligned");
   args.n = 1;
   if ((s = check_device())) return s;
   if (a_fmt != RL_A_BF16) return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
-  const Plan8 p = plan8(M, N, device_cus());
   int total = 0;
+  if (workspace) {
+    const SplitPlan sp = plan_split(M, N, K, device_cus());
+    if (sp.ks > 1) {
+      if (sp.ws_bytes > workspace_bytes)
+        return fail(RL_ERR_WORKSPACE, "workspace %lld bytes, this shape needs %lld (rl_bfp16_gemm_workspace_bytes)",
+                    (long long)workspace_bytes, (long long)sp.ws_bytes);
+      args.d[0].ksplit = sp.ks;
+      args.d[0].part = static_cast<float*>(workspace);
+      set_tiles8(args, sp.mf, total);
+      if ((s = launch8<1>(args, total, sp.mf, stream))) return s;
+      const int64_t nblocks = M * ((ep && ep->act == RL_ACT_SWIGLU) ? N / 2 : N) / 8;
+      hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0,
+                         static_cast<hipStream_t>(stream), args.d[0]);
+      return launch_status("rl_bfp16_gemm (reduce)");
+    }
+  }
+  const Plan8 p = plan8(M, N, device_cus());
   if (p.split == 0) {
     set_tiles8(args, p.mf, total);
     return launch8<1>(args, total, p.mf, stream);
@@ -985,6 +1153,11 @@ int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_pa
   if ((s = launch8<1>(args, total, p.mf, stream))) return s;
   set_tiles8(tail, p.mf_tail, total);
   return launch8<1>(tail, total, p.mf_tail, stream);
+}
+
+int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* stream) {
+  return rl_bfp16_gemm_ws(A, a_fmt, lda, B_packed, C, ldc, M, N, K, ep, nullptr, 0, stream);
 }
 
 int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, void* stream) {

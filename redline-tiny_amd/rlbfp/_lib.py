@@ -52,6 +52,9 @@ SIGNATURES = {
     "rl_bfp16_quantize": (ctypes.c_int, [_P, _I32, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "rl_bfp16_dequantize": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _P]),
     "rl_bfp16_gemm": (ctypes.c_int, [_P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue), _P]),
+    "rl_bfp16_gemm_ws": (ctypes.c_int, [_P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue),
+                                        _P, _I64, _P]),
+    "rl_bfp16_gemm_workspace_bytes": (ctypes.c_int64, [_I64, _I64, _I64]),
     "rl_bfp16_gemm_grouped": (ctypes.c_int, [ctypes.POINTER(GemmDesc), _I32, _I32, _P]),
     "rl_bfp16_gemv": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "rl_ln_modulate": (ctypes.c_int, [_P, _I64, _P, _I32, _I64, _P, _I64, _I32, _P, _I64, _P, _I32, _P, _I64, _I64,

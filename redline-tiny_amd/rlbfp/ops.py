@@ -134,10 +134,25 @@ def _a_args(a, a_fmt, M, K):
     return K
 
 
+_GEMM_WS = {}
+
+
+def gemm_workspace_bytes(M, N, K, device=None):
+    """Bytes of the K-split workspace of an RL_A_BF16 GEMM of this shape (0: it runs whole); cached per shape."""
+    key = (M, N, K, torch.cuda.current_device() if device is None else torch.device(device).index)
+    if key not in _GEMM_WS:
+        n = L.lib().rl_bfp16_gemm_workspace_bytes(M, N, K)
+        if n < 0:
+            raise ValueError(f"invalid GEMM shape M={M} N={N} K={K}")
+        _GEMM_WS[key] = n
+    return _GEMM_WS[key]
+
+
 def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None, gate_split_row=0,
-         residual=None, quantize_out=False, out=None):
+         residual=None, quantize_out=False, out=None, split=True):
     """C = epilogue(A @ B) with B the packed weight stream of a (K, N) matrix, bf16 output (M, N) (or (M, N/2) for
-    act="swiglu"). See rl_bfp16_gemm in include/rlbfp.h for the epilogue order."""
+    act="swiglu"). See rl_bfp16_gemm in include/rlbfp.h for the epilogue order. split: let a small-M, deep-K GEMM
+    split K into pieces (rl_bfp16_gemm_ws, workspace from torch's allocator); False: always the whole-K kernel."""
     _dev(a, "A")
     _dev(b_packed, "B")
     if M is None:
@@ -154,8 +169,14 @@ def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None
         raise ValueError(f"out must be ({M}, {nout}) bfloat16 with unit column stride")
     _check_ep_sizes(M, N, nout, bias, gate, gate_split_row, residual)
     ep = _epilogue(act, bias, gate, gate_split_row, residual, quantize_out)
-    L.check(L.lib().rl_bfp16_gemm(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M, N, K,
-                                  ctypes.byref(ep), _stream(a)))
+    nws = gemm_workspace_bytes(M, N, K, a.device) if split and a_fmt == "bf16" else 0
+    if nws:
+        ws = torch.empty(nws, dtype=torch.uint8, device=a.device)
+        L.check(L.lib().rl_bfp16_gemm_ws(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M,
+                                         N, K, ctypes.byref(ep), _ptr(ws), nws, _stream(a)))
+    else:
+        L.check(L.lib().rl_bfp16_gemm(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M, N,
+                                      K, ctypes.byref(ep), _stream(a)))
     return out
 
 

@@ -2,6 +2,8 @@
 max |ref| <= 1e-2 (the reference's error metric, redline/run_glue.py:158-159), and element-wise within a bf16 ulp
 plus the fp32 summation difference."""
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -187,3 +189,72 @@ def test_tile_plans(dev, M, N):
     ref = np.where((rows < split)[:, None], G.gemm_ref(Aq[rows], Bq, gate=gate[[1, 1]], residual=res[rows]),
                    G.gemm_ref(Aq[rows], Bq, gate=gate[[0, 0]], residual=res[rows]))
     check(out[torch.from_numpy(rows).cuda()], ref)
+
+
+def _split_case(M, K, N, seed, act=None):
+    rng = np.random.default_rng(seed)
+    A = G.activations(rng, M, K)
+    if act == "swiglu":
+        packed = F.pack_b(F.interleave_up(G.linear_weight(rng, N // 2, K), G.linear_weight(rng, N // 2, K)))
+    else:
+        packed = F.pack_b(G.linear_weight(rng, N, K).T)
+    return rng, F.quantize_rows(A), packed, F.decode_b(packed, K, N)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 8192, 512), (100, 4096, 384), (512, 3072, 3072)])
+def test_k_split_plain(dev, M, K, N):
+    """Small-M, deep-K shapes split K into pieces (fp32 partials in a workspace, summed in piece order): against the
+    emulation, and against the whole-K kernel to within the fp32 summation difference."""
+    assert ops.gemm_workspace_bytes(M, N, K) > 0
+    rng, Aq, packed, Bq = _split_case(M, K, N, M + K)
+    a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)
+    out = ops.gemm(a, b, N, K)
+    whole = ops.gemm(a, b, N, K, split=False)
+    ref = G.gemm_ref(Aq, Bq)
+    check(out, ref)
+    d = (out.float() - whole.float()).abs().cpu().numpy()
+    assert (d <= np.abs(ref) * 2.0 ** -7 + 1e-5 * np.abs(ref).max()).all()
+
+
+def test_k_split_epilogues(dev):
+    """Every epilogue after the piece reduction: bias + GELU, SwiGLU with bias and re-quantize, gate rows split
+    with residual."""
+    M, K, N = 256, 8192, 512
+    rng, Aq, packed, Bq = _split_case(M, K, N, 21)
+    a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)
+    bias = (rng.standard_normal(N) * 0.5).astype(np.float32)
+    out = ops.gemm(a, b, N, K, bias=dev_t(bias, torch.float32), act="gelu_tanh")
+    check(out, G.gemm_ref(Aq, Bq, bias=bias, act=G.ACT_GELU_TANH))
+    res = F.bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    gate = rng.standard_normal((2, N)).astype(np.float32)
+    out = ops.gemm(a, b, N, K, gate=dev_t(gate, torch.float32), gate_split_row=100, residual=dev_t(res, torch.bfloat16))
+    check(out, G.gemm_ref(Aq, Bq, gate=gate, gate_split_row=100, residual=res))
+    rng, Aq, packed, Bq = _split_case(M, K, N, 22, act="swiglu")
+    bias = (rng.standard_normal(N) * 0.1).astype(np.float32)
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, act="swiglu",
+                   bias=dev_t(bias, torch.float32), quantize_out=True)
+    assert out.shape == (M, N // 2)
+    check(out, G.gemm_ref(Aq, Bq, act=G.ACT_SWIGLU, bias=bias, quantize_out=True), tol=2e-2)
+    o = out.float().cpu().numpy()
+    assert (F.quantize_rows(o) == o).mean() > 0.999  # exact bfp16 blocks (the -128 corner aside)
+
+
+def test_k_split_workspace(dev):
+    """The workspace contract: a shape the planner keeps whole needs none; too small a workspace is RL_ERR_WORKSPACE;
+    a NULL workspace runs the whole-K kernel (same bits as rl_bfp16_gemm)."""
+    from rlbfp import _lib as L
+    assert ops.gemm_workspace_bytes(4352, 24576, 3072) == 0
+    M, K, N = 100, 4096, 384
+    need = ops.gemm_workspace_bytes(M, N, K)
+    assert need == L.lib().rl_bfp16_gemm_workspace_bytes(M, N, K) > 0
+    rng, Aq, packed, Bq = _split_case(M, K, N, 23)
+    a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    ep = ops._epilogue(None, None, None, 0, None, False)
+    st = torch.cuda.current_stream().cuda_stream
+    args = (a.data_ptr(), 0, K, b.data_ptr(), out.data_ptr(), N, M, N, K, ctypes.byref(ep))
+    assert L.lib().rl_bfp16_gemm_ws(*args, ws.data_ptr(), need - 16, st) == L.RL_ERR_WORKSPACE
+    assert L.lib().rl_bfp16_gemm_ws(*args, None, 0, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, ops.gemm(a, b, N, K, split=False))

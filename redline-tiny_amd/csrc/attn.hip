@@ -63,7 +63,6 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (the lane groups holding one query's keys), with the
 // gfx950 row-swap permutes instead of LDS round trips: permlane16_swap(x, x) yields rows {0,0,2,2} and {1,1,3,3},
@@ -88,11 +87,6 @@ __device__ __forceinline__ float sum4(float v) {
 // most blocks skip the rescale of O; P then stays below 2^8 (exact enough in fp32, rounded to bf16 like any P).
 constexpr float kAtRebase = 8.0f;
 
-// two floats -> packed bf16, round to nearest even (one v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 // Swizzle of the 16-byte chunks of V^T row dim (only dim % 16 matters)
 __device__ __forceinline__ int vswz(int dim) { return ((dim >> 1) & 7) ^ (dim & 1); }
@@ -272,9 +266,9 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
         // P^T operand for 32-key step c: keys 32c + 4 lg + 0..3 (group 2c), then 32c + 16 + 4 lg + 0..3 (group 2c + 1)
 #pragma unroll
         for (int c = 0; c < 2; c++)
-          Pb[s][c] = u32x4{pack_bf16(S[s][2 * c][0], S[s][2 * c][1]), pack_bf16(S[s][2 * c][2], S[s][2 * c][3]),
-                           pack_bf16(S[s][2 * c + 1][0], S[s][2 * c + 1][1]),
-                           pack_bf16(S[s][2 * c + 1][2], S[s][2 * c + 1][3])};
+          Pb[s][c] = u32x4{pack_bf16_rne(S[s][2 * c][0], S[s][2 * c][1]), pack_bf16_rne(S[s][2 * c][2], S[s][2 * c][3]),
+                           pack_bf16_rne(S[s][2 * c + 1][0], S[s][2 * c + 1][1]),
+                           pack_bf16_rne(S[s][2 * c + 1][2], S[s][2 * c + 1][3])};
         // the row sum from the same bf16 P the second product uses
         const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
@@ -392,8 +386,8 @@ __global__ __launch_bounds__(W * 64, 8 / W) void attn_kernel(AttnArgs a) {
           *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) = uint2{b[0] | (b[1] << 16), b[2] | (b[3] << 16)};
         } else {
           *reinterpret_cast<uint2*>(orow + 16 * dg + 4 * lg) =
-              uint2{pack_bf16(__uint_as_float(u[0]), __uint_as_float(u[1])),
-                    pack_bf16(__uint_as_float(u[2]), __uint_as_float(u[3]))};
+              uint2{pack_bf16_rne(__uint_as_float(u[0]), __uint_as_float(u[1])),
+                    pack_bf16_rne(__uint_as_float(u[2]), __uint_as_float(u[3]))};
         }
       }
     }
@@ -478,10 +472,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs c) {
         u32x4{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
   } else {
     *reinterpret_cast<u32x4*>(orow) =
-        u32x4{pack_bf16(__uint_as_float(uu[0]), __uint_as_float(uu[1])),
-              pack_bf16(__uint_as_float(uu[2]), __uint_as_float(uu[3])),
-              pack_bf16(__uint_as_float(uu[4]), __uint_as_float(uu[5])),
-              pack_bf16(__uint_as_float(uu[6]), __uint_as_float(uu[7]))};
+        u32x4{pack_bf16_rne(__uint_as_float(uu[0]), __uint_as_float(uu[1])),
+              pack_bf16_rne(__uint_as_float(uu[2]), __uint_as_float(uu[3])),
+              pack_bf16_rne(__uint_as_float(uu[4]), __uint_as_float(uu[5])),
+              pack_bf16_rne(__uint_as_float(uu[6]), __uint_as_float(uu[7]))};
   }
 }
 

@@ -91,12 +91,6 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * u2));
 }
 
-// float32 -> bf16 bits, round half to even (finite inputs).
-__device__ __forceinline__ uint32_t bf16_rne(float v) {
-  const uint32_t u = __float_as_uint(v);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-
 // Re-quantize one block of 8 bf16 values (4 packed words) to bfp16, returned as bf16 words: the encoder's float fast
 // path (encode_fast / decode_fast: one exact power-of-two scaling and one half-to-even rounding per value) for block
 // exponents 7..237, the integer encoder otherwise, so the result equals the integer encoder's and does not depend on
@@ -145,10 +139,8 @@ __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int oc
       v[k] = rk + gk * v[k];
     }
   }
-  uint32_t b[8];
-#pragma unroll
-  for (int k = 0; k < 8; k++) b[k] = bf16_rne(v[k]);
-  u32x4 o = {b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
+  u32x4 o = {pack_bf16_rne(v[0], v[1]), pack_bf16_rne(v[2], v[3]), pack_bf16_rne(v[4], v[5]),
+             pack_bf16_rne(v[6], v[7])};
   if (d.flags & RL_EP_QUANTIZE_OUT) o = requantize8(o);
   return o;
 }

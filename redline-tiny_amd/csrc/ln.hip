@@ -49,14 +49,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// two floats -> one word of two bf16, each rounded to nearest even (one v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
-  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 __device__ __forceinline__ void unpack8(u32x4 v, float f[8]) {
   f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xFFFF0000u);
   f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xFFFF0000u);

@@ -10,6 +10,13 @@
 namespace rl {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// two floats -> one word of two bf16 (lo in bits 0..15), each rounded to nearest even: one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -47,6 +47,20 @@ __device__ __forceinline__ void unpack8f(u32x4 v, float f[8]) {
   f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xFFFF0000u);
 }
 
+// Sum over each row of 16 lanes, every lane of the row getting the same value: quad swaps, then half-row and row
+// mirrors, each one v_add_f32 with a DPP operand (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);  // row_half_mirror: lane i <- 7 - i within each 8
+  v += dpp_f<0x140>(v);  // row_mirror: lane i <- 15 - i
+  return v;
+}
+
 __device__ __forceinline__ void stage_block(uint8_t* stage, int pos, uint32_t E, const int32_t q[8]) {
   uint8_t* p = stage + pos * kBlockBytes;
   p[0] = (uint8_t)E;
@@ -54,6 +68,8 @@ __device__ __forceinline__ void stage_block(uint8_t* stage, int pos, uint32_t E,
   for (int e = 0; e < 8; e++) p[1 + e] = (uint8_t)(int8_t)q[e];
 }
 
+// TILES / NATIVE: whether any tile / any head-major bf16 output is requested (the other's work is compiled out).
+template <bool TILES, bool NATIVE>
 __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stage[kTile9];
   const int tid = threadIdx.x;
@@ -63,14 +79,14 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
   const int64_t row0 = (int64_t)t * kTileTokens;
   const int64_t D = (int64_t)a.heads * kHeadDim;
   const int64_t col0 = part * D + h * kHeadDim;
-  const bool tiles = part == 0 ? a.q_tiles != nullptr : a.kv_tiles != nullptr;
+  const bool tiles = TILES && (part == 0 ? a.q_tiles != nullptr : a.kv_tiles != nullptr);
 
   if (part < 2) {
     // Q (part 0) and K (part 1): thread = (token rr + 16 pass, dim block bc)
     const int bc = tid & 15, rr = tid >> 4;
     float wf[8];
     unpack8f(*reinterpret_cast<const u32x4*>((part ? a.wk : a.wq) + bc * 8), wf);
-    uint16_t* nat = part ? a.k : a.q;
+    uint16_t* nat = NATIVE ? (part ? a.k : a.q) : nullptr;
 #pragma unroll
     for (int pass = 0; pass < 4; pass++) {
       const int r = pass * 16 + rr;
@@ -80,9 +96,8 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) ss = fmaf(xf[e], xf[e], ss);
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);  // the token's 16 lanes
-      const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + 1e-6f);
+      ss = row16_sum(ss);  // the token's 16 lanes
+      const float inv = __builtin_amdgcn_rsqf(ss / (float)kHeadDim + 1e-6f);
       const uint2 cr = *reinterpret_cast<const uint2*>(a.cos + row * 64 + bc * 4);
       const uint2 sr = *reinterpret_cast<const uint2*>(a.sin + row * 64 + bc * 4);
       const float c4[4] = {__uint_as_float(cr.x << 16), __uint_as_float(cr.x & 0xFFFF0000u),
@@ -116,7 +131,7 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; e++) u[e] = (uint32_t)a.C[(row0 + kb * 8 + e) * a.ldc + col0 + d] << 16;
       const uint32_t E = encode_block(u, q, bw);
-      if (a.v)  // V^T: the block's 8 tokens are contiguous in row d
+      if (NATIVE && a.v)  // V^T: the block's 8 tokens are contiguous in row d
         *reinterpret_cast<u32x4*>(a.v + ((int64_t)h * kHeadDim + d) * a.M + row0 + kb * 8) = bw;
       if (tiles) stage_block(stage, (((d >> 4) * 8 + kb) * 2 + ((d >> 3) & 1)) * 8 + (d & 7), E, q);
     }
@@ -151,6 +166,13 @@ extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t he
   a.cos = cos; a.sin = sin; a.wq = wq; a.wk = wk;
   a.q_tiles = q_tiles; a.kv_tiles = kv_tiles; a.q = q; a.k = k; a.v = v;
   const dim3 grid((unsigned)(M / kTileTokens * heads * 3));
-  hipLaunchKernelGGL(qkv_post_kernel, grid, dim3(kQkvThreads), 0, static_cast<hipStream_t>(stream), a);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool tiles = q_tiles || kv_tiles, native = q || k || v;
+  if (tiles && native)
+    hipLaunchKernelGGL((qkv_post_kernel<true, true>), grid, dim3(kQkvThreads), 0, st, a);
+  else if (tiles)
+    hipLaunchKernelGGL((qkv_post_kernel<true, false>), grid, dim3(kQkvThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((qkv_post_kernel<false, true>), grid, dim3(kQkvThreads), 0, st, a);
   return launch_status("rl_qkv_post");
 }

@@ -43,9 +43,20 @@ struct LnArgs {
   int32_t rows_wg;  // rows per workgroup: 4, or 16 for the A-layout order
 };
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the wave, every lane getting the same value: within rows of 16 by DPP adds (quad swaps, half-row and row
+// mirrors), then across the four rows with two lane permutes.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
   return v;
 }
 
@@ -139,7 +150,7 @@ __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel
       }
     }
     ss = wave_sum(ss);
-    const float rstd = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+    const float rstd = __builtin_amdgcn_rsqf(ss / (float)D + 1e-6f);
 
     // y = (x' - mean) * rstd * sc -> bfp16
 #pragma unroll

@@ -36,7 +36,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (vendor figure)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # HBM bytes per up-GEMM launch from rocprofv3 FETCH_SIZE (x2) and WRITE_SIZE (x1), the factors that make a 256 MB
 # device-to-device copy read and write 256 MB (profiles/gemm_dit_ffn_counters.md); re-measured when the kernel changes
-UP_GEMM_TRAFFIC_BYTES = 978831065
+UP_GEMM_TRAFFIC_BYTES = 978832537
 M, K, FF = 4352, 3072, 12288
 GEMV_K, GEMV_N = 3072, 18432
 
@@ -88,7 +88,7 @@ class Timer:
         return ts[n // 2] if n % 2 else 0.5 * (ts[n // 2 - 1] + ts[n // 2])
 
 
-def gpu_bench(steps, warmup):
+def gpu_bench(steps, warmup, no_configs=False):
     import torch
 
     from rlbfp import ops
@@ -216,7 +216,7 @@ def gpu_bench(steps, warmup):
         "ln": ln_bench(dev),
         "qkv": qkv_bench(dev),
         "attn": attn_bench(dev),
-        "configs": configs_bench(dev),
+        "configs": None if no_configs else configs_bench(dev),
     }
 
 
@@ -565,6 +565,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' GEMM timings")
     ap.add_argument("--sustain", type=float, default=0, metavar="SECONDS",
                     help="only run the up GEMM, then torch's bf16 linear of the same shape, back to back for SECONDS "
                          "each while amd-smi reads socket power and graphics clock; print one line per kernel and exit")
@@ -582,7 +583,7 @@ def main():
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by weight columns, "
               "see DESIGN.md, but multi-GPU runs are not part of this build)", file=sys.stderr)
         sys.exit(2)
-    r = gpu_bench(args.steps, args.warmup)
+    r = gpu_bench(args.steps, args.warmup, args.no_configs)
     ms_step = r["ms_step"]
     step_flops = flops_up() + flops_down()
     up_tflops = flops_up() / (r["ms_up"] * 1e-3) / 1e12

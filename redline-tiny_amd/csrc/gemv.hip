@@ -18,6 +18,11 @@ constexpr int kVWaves = 3;                    // waves per workgroup; they split
 constexpr int kVThreads = 64 * kVWaves;
 constexpr int kVIterBytes = 8 * 1152;         // one wave iteration: 8 K tiles of one 16-column group = 9 x 1 KB
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
 __device__ __forceinline__ float silu_v(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
@@ -200,23 +205,35 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
     float v[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) v[j] = part[m][j];
-    int cnt = 16;
+    // bits 5 and 4: the row-swap permutes exchange (v[i], v[i + hv]) between the halves, so each lane gets its own
+    // kept value and its partner's sent one, with no selects and no LDS
 #pragma unroll
-    for (int sb = 32; sb >= 4; sb >>= 1) {
-      const int hv = cnt / 2;
-      const bool up = (lane & sb) != 0;
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        if (i < hv) {
-          const float send = up ? v[i] : v[i + hv];
-          const float keep = up ? v[i + hv] : v[i];
-          v[i] = keep + __shfl_xor(send, sb);
-        }
-      }
-      cnt = hv;
+    for (int i = 0; i < 8; i++) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 8]), false, false);
+      v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
-    float t = v[0] + __shfl_xor(v[0], 2);
-    t += __shfl_xor(t, 1);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false, false);
+      v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    // bit 3 (partner lane ^ 8: a row rotation by 8) and bit 2 (partner 7 - i within 8, the half-row mirror: the
+    // quad sums below still cover all 8 lanes), each lane sending one value and keeping the other
+    {
+      const bool up = (lane & 8) != 0;
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const float send = up ? v[i] : v[i + 2], keep = up ? v[i + 2] : v[i];
+        v[i] = keep + dpp_f<0x128>(send);  // row_ror:8
+      }
+    }
+    {
+      const bool up = (lane & 4) != 0;
+      const float send = up ? v[0] : v[1], keep = up ? v[1] : v[0];
+      v[0] = keep + dpp_f<0x141>(send);  // row_half_mirror
+    }
+    float t = v[0] + dpp_f<0x4E>(v[0]);  // quad_perm [2, 3, 0, 1]
+    t += dpp_f<0xB1>(t);                 // quad_perm [1, 0, 3, 2]
     if ((lane & 3) == 0) red[wave][m][col] = t;
   }
   __syncthreads();

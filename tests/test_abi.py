@@ -165,3 +165,29 @@ def test_validate_attention(args, code):
 
 def test_attention_null_pointers_rejected_before_any_gpu_call():
     assert L.lib().rl_attention(None, None, None, 1, 128, 64, 64, None, None, 128, 0, 0, None) == L.RL_ERR_NULL
+
+
+def test_gemm_split_plan_without_a_gpu():
+    """The K-split planner behind rl_bfp16_gemm_workspace_bytes (256 compute units when no device is visible, as on
+    MI355X): the text encoder's down projection at M = 512 splits 4 ways with 128-row tiles (4 x 512 x 4096 fp32
+    planes); shapes whose tiles fill the chip, and shallow K, run whole; invalid shapes give -1."""
+    ws = L.lib().rl_bfp16_gemm_workspace_bytes
+    if _has_gpu():
+        pytest.skip("the plan depends on the visible device's compute units")
+    assert ws(512, 4096, 12288) == 4 * 512 * 4096 * 4
+    for M, N, K in ((4352, 24576, 3072), (4352, 3072, 12288), (4096, 3072, 3072), (512, 24576, 4096), (1, 128, 64)):
+        assert ws(M, N, K) == 0, (M, N, K)
+    assert ws(512, 100, 64) == -1  # N % 128 != 0
+    assert ws(0, 128, 64) == -1
+
+
+def test_gemm_ws_null_pointers_rejected_before_any_gpu_call():
+    assert L.lib().rl_bfp16_gemm_ws(None, 0, 64, None, None, 128, 1, 128, 64, None, None, 0, None) == L.RL_ERR_NULL
+
+
+def _has_gpu():
+    try:
+        import torch
+        return torch.cuda.device_count() > 0
+    except Exception:
+        return False

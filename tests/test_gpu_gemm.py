@@ -258,3 +258,49 @@ def test_k_split_workspace(dev):
     assert L.lib().rl_bfp16_gemm_ws(*args, None, 0, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(out, ops.gemm(a, b, N, K, split=False))
+
+
+def _exponent_class_weight(rng, N, K, classes):
+    """Linear weight (N, K) whose column n of B = W.T holds blocks of exponent class classes[n % len(classes)]: E (all
+    8 values in the binade [2^(E-127), 2^(E-126)), so every q is in 64..127 and every decoded value is a normal
+    number), None (all-zero blocks) or "ordinary" (the usual ~N(0, 0.02) weights)."""
+    W = G.linear_weight(rng, N, K)
+    for n in range(N):
+        E = classes[n % len(classes)]
+        if E == "ordinary":
+            continue
+        if E is None:
+            W[n] = 0.0
+            continue
+        mag = rng.uniform(1.0, 1.49, K)
+        mag[::8] = 1.5  # one block maximum per block
+        W[n] = mag * rng.choice([-1.0, 1.0], K) * 2.0 ** (E - 127)
+    return W.astype(np.float32)
+
+
+@pytest.mark.parametrize("classes,a_scale", [((1, 3, 6, 7, 8, None, "ordinary"), 2.0 ** 100),
+                                             ((133, 134, 200, 220, None, "ordinary"), 1.0)])
+def test_weight_block_exponents(dev, classes, a_scale):
+    """Weight blocks at the edges of the decoder's fast exponent range (E = 7..133, by a packed exponent subtract)
+    and past them (E = 1, 3, 6, 134, 200, 220, and all-zero blocks, which the float path re-decodes). Columns of one
+    class sit next to columns of others, so a decoding lane covers several classes; A is scaled by a power of two so
+    that every product is a normal number; each column is checked against the emulation at its own scale."""
+    M, K, N = 256, 512, 256
+    rng = np.random.default_rng(31)
+    Aq = F.quantize_rows(G.activations(rng, M, K)) * np.float32(a_scale)
+    W = _exponent_class_weight(rng, N, K, classes)
+    packed = F.pack_b(W.T)
+    want_E = {c for c in classes if isinstance(c, int)} | ({0} if None in classes else set())
+    assert want_E <= set(packed.reshape(-1, 9)[:, 0].tolist())
+    Bq = F.decode_b(packed, K, N)
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K).float().cpu().numpy()
+    ref = G.gemm_ref(Aq, Bq)
+    assert np.isfinite(ref).all()
+    for n in range(N):
+        got, want = out[:, n].astype(np.float64), ref[:, n]
+        scale = np.abs(want).max()
+        if scale == 0:
+            assert (got == 0).all(), n  # all-zero column
+            continue
+        assert np.abs(got - want).max() <= TOL * scale, (n, classes[n % len(classes)])
+        assert (np.abs(got - want) <= 2 * np.abs(want) * 2.0 ** -8 + 1e-4 * scale).mean() > 0.99, n

@@ -16,7 +16,7 @@
 //     16-byte-chunk XOR swizzle; all four waves read it as ds_read_b128 operands.
 //   * loads run two K steps ahead: while the MFMAs of step k run, the raw B windows and the A chunks of step k+1
 //     are in flight; after them B(k+1) is decoded and A(k+1) stored to the other LDS stage.
-//   * workgroups are remapped so each XCD walks a contiguous range of tiles, grouped 8 M-tiles at a time.
+//   * workgroups are remapped so each XCD walks a contiguous range of tiles, grouped kGroupM M-tiles at a time.
 #include <math.h>
 #include <stdio.h>
 
@@ -30,7 +30,9 @@ constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int kGThreads = 256;
 constexpr int kAStage = BM * BK * 2;  // bytes of one A stage
 constexpr int kTileBytes = 64 * 128 * 9 / 8;  // one b_layout tile (64 K x 128 N)
-constexpr int kGroupM = 8;
+// Tiles are walked kGroupM M-tiles at a time within each XCD's contiguous range: the 32 CUs of an XCD then hold a
+// block of 4 M-tiles x 8 N-tiles, which fetches fewer A + B bytes through L2 than 8 x 4 (A tiles are the larger ones).
+constexpr int kGroupM = 4;
 
 struct GemmDesc {
   const void* A;

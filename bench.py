@@ -454,20 +454,42 @@ def cpu_baseline(host, p_up, p_down, rows=M, runs=3):
         assert out.shape == (rows, K)
         return time.perf_counter() - t0
 
+    # the BLAS pool is set to the host cores this process may use: the CPU share the environment states
+    # (OMP_NUM_THREADS), else the affinity mask
+    visible = len(os.sched_getaffinity(0))
+    cores = min(visible, int(os.environ.get("OMP_NUM_THREADS") or visible))
+    blas, blas_threads = "unknown", None
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+        limiter = threadpool_limits(limits=cores, user_api="blas")
+        pools = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        if pools:
+            blas = f"{pools[0].get('internal_api')} {pools[0].get('version')} ({os.path.basename(pools[0].get('filepath', ''))})"
+            blas_threads = pools[0].get("num_threads")
+    except Exception:
+        limiter = None
     one()                                        # warm-up
     dt = sorted(one() for _ in range(runs))[runs // 2]
+    if limiter is not None:
+        limiter.restore_original_limits()
     flops = 2.0 * rows * K * 2 * FF + 2.0 * rows * FF * K
-    threads = None
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads") or 0) for i in threadpool_info()) or None
-    except Exception:
-        pass
-    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s",
-            "cores": threads or len(os.sched_getaffinity(0)), "kind": "port",
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": blas_threads or cores, "kind": "port",
+            "blas": blas, "blas_threads": blas_threads, "cpu_model": _cpu_model(), "cpus_visible": visible,
             "sample": f"the full FFN pair step ({rows} rows, weights decoded from the packed bytes each run), median "
-                      f"of {runs} runs after a warm-up, {dt:.2f} s per step; numpy float32 BLAS, "
-                      f"{len(os.sched_getaffinity(0))} host cpus visible"}
+                      f"of {runs} runs after a warm-up, {dt:.2f} s per step; numpy float32 BLAS matmuls on "
+                      f"{blas_threads or cores} threads"}
+
+
+def _cpu_model():
+    """The host CPU's model name from /proc/cpuinfo (None if unreadable)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def copy_probe(mb, reps=10):

@@ -100,19 +100,29 @@ typedef struct rl_epilogue {
 int rl_bfp16_gemm(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
                   int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *stream);
 
-/* rl_bfp16_gemm with a caller's workspace (device memory, 16-byte aligned), which lets a GEMM whose output tiles fill
- * few compute units (small M, deep K: the text encoder's down projection at M = 512, K = 12288) split K into pieces
- * that run side by side. Each piece writes fp32 partial sums to the workspace; a second launch adds them in piece
- * order and applies the epilogue as above (results differ from the whole-K sums by fp32 rounding only). Only
- * RL_A_BF16 splits. workspace NULL, or a shape the planner keeps whole: exactly rl_bfp16_gemm. workspace_bytes below
- * rl_bfp16_gemm_workspace_bytes(): RL_ERR_WORKSPACE. Calls that share a workspace on different streams race. Same
- * reference interface as rl_bfp16_gemm (redline/forward.py:194-197). */
+/* rl_bfp16_gemm with a caller's workspace (device memory, 16-byte aligned). It serves two purposes:
+ *   - a GEMM whose output tiles fill few compute units (small M, deep K: the text encoder's down projection at
+ *     M = 512, K = 12288) may split K into pieces that run side by side. Each piece writes fp32 partial sums to the
+ *     workspace; a second launch adds them in piece order and applies the epilogue as above (results differ from
+ *     the whole-K sums by fp32 rounding only);
+ *   - an A in any format other than RL_A_BF16 (the NPU's packed A layout above all: every GEMM of
+ *     redline/forward.py passes A that way, :32, :245) is first staged as bf16 in the workspace (its exact bfp16
+ *     values, one HBM-bound pass: 9/8 + 2 bytes per value), and the product then runs on the RL_A_BF16 kernel with
+ *     the rest of the workspace. The result is the RL_A_BF16 path's on the staged values: bit-identical to
+ *     rl_bfp16_gemm's for the same format unless the K split applies.
+ * workspace NULL: exactly rl_bfp16_gemm (a non-bf16 A then takes the register-staged kernel, which is slower).
+ * workspace_bytes below what rl_bfp16_gemm_workspace_size() gives for the shape and format: RL_ERR_WORKSPACE for a
+ * non-bf16 A that the staged copy does not fit; otherwise the planner runs whole K. Calls that share a workspace on
+ * different streams race. Same reference interface as rl_bfp16_gemm (redline/forward.py:194-197). */
 int rl_bfp16_gemm_ws(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
                      int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *workspace, int64_t workspace_bytes,
                      void *stream);
 /* Workspace bytes rl_bfp16_gemm_ws needs for an RL_A_BF16 GEMM of this shape on the current device (0: this shape
  * runs whole; -1: the shape is invalid). */
 int64_t rl_bfp16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+/* Workspace bytes rl_bfp16_gemm_ws uses for this A format and shape: the staged bf16 A for a non-bf16 format
+ * (M * K * 2 rounded up to 256), plus the K-split partials; -1: invalid shape or format. */
+int64_t rl_bfp16_gemm_workspace_size(int32_t a_fmt, int64_t M, int64_t N, int64_t K);
 
 /* Several independent GEMMs (different shapes, weights and epilogues, one A format) in one launch, e.g. the image-
  * and text-stream projections of a DiT block. At most RL_MAX_GROUP descriptors. Replaces the per-op sequence of
@@ -186,6 +196,15 @@ int rl_qkv_post(const uint16_t *C, int64_t ldc, int64_t M, int32_t heads, const 
                 const uint16_t *wq, const uint16_t *wk, uint8_t *q_tiles, uint8_t *kv_tiles, uint16_t *q, uint16_t *k,
                 uint16_t *v, void *stream);
 
+/* rl_qkv_post for grouped-query attention: C (M, (hq + 2 hkv) * 128) holds per token row the q columns of hq heads,
+ * then the k and v columns of hkv heads each. Outputs as above with hq Q heads and hkv K / V heads: q_tiles (hq, M/64,
+ * 9216), kv_tiles (hkv, M/64, 2, 9216), q (hq, M, 128), k (hkv, M, 128), v (hkv, 128, M). hq == hkv is rl_qkv_post.
+ * Replaces the text encoder's GQA QKV-post artifacts (kernels/vlm/qkv_gqa_design.py, 32 q and 8 kv heads, with the
+ * same microkernels kernels/glue/qkv_post.cc) run by LM._layer (redline/vlm_run.py:433-437). */
+int rl_qkv_post_gqa(const uint16_t *C, int64_t ldc, int64_t M, int32_t hq, int32_t hkv, const uint16_t *cos,
+                    const uint16_t *sin, const uint16_t *wq, const uint16_t *wk, uint8_t *q_tiles, uint8_t *kv_tiles,
+                    uint16_t *q, uint16_t *k, uint16_t *v, void *stream);
+
 /* ---- attention over the QKV post pass's output -------------------------------------------------------------------
  * Per head h and query i: O[i][(h0 + h) * 128 + d] = sum_j P[i][j] V[j][d], P = 2^(S - max) / sum over the visible
  * keys, S = Q K^T. Q carries the score scale log2(e)/sqrt(128) (as rl_qkv_post's wq does), so S is in log2 units.
@@ -222,6 +241,7 @@ int64_t rl_attention_workspace_bytes(int32_t heads, int64_t nq, int64_t nk);
 int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int64_t ld_xo, int32_t a_order,
                    int64_t ld_a, int64_t split_row, int64_t M, int64_t D);
 int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads);
+int rl_validate_qkv_post_gqa(int64_t ldc, int64_t M, int32_t hq, int32_t hkv);
 int rl_validate_attention(int32_t heads, int64_t nq, int64_t nk, int64_t nkv, int64_t ldo, int32_t h0);
 int rl_validate_quantize(int32_t x_dtype, int64_t rows, int64_t cols, int64_t ld_x, int32_t order);
 int rl_validate_gemm(int32_t a_fmt, int64_t lda, int64_t ldc, int64_t M, int64_t N, int64_t K, const rl_epilogue *ep);

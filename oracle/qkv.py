@@ -84,16 +84,19 @@ def qkv_table_loop(cos, sin, wqc, wk, t0):
     return F.bf16_round(np.concatenate([tab.reshape(-1), wqc, wk]))
 
 
-def qkv_post_ref(C, cos, sin, wqc, wk, heads):
-    """C (M, 3 * heads * 128) float values; cos/sin (M, 64); wqc, wk (128). -> (Q, K, V) float64, each
-    (heads, M, 128), before quantization."""
+def qkv_post_ref(C, cos, sin, wqc, wk, heads, kv_heads=None):
+    """C (M, (heads + 2 kv_heads) * 128) float values, columns [q heads | k kv_heads | v kv_heads] (kv_heads None:
+    = heads; fewer for the text encoder's grouped-query attention, kernels/vlm/qkv_gqa_design.py:1-10); cos/sin
+    (M, 64); wqc, wk (128). -> (Q (heads, M, 128), K, V (kv_heads, M, 128)) float64, before quantization."""
     C = np.asarray(C, np.float64)
     cos, sin = np.asarray(cos, np.float64), np.asarray(sin, np.float64)
     wqc, wk = np.asarray(wqc, np.float64), np.asarray(wk, np.float64)
-    d, hd = heads * HEAD_DIM, HEAD_DIM
+    hkv = heads if kv_heads is None else kv_heads
+    hd = HEAD_DIM
+    dq, dk = heads * hd, hkv * hd
     Q = np.stack([rms_rope(C[:, h * hd:(h + 1) * hd], wqc, cos, sin) for h in range(heads)])
-    K = np.stack([rms_rope(C[:, d + h * hd:d + (h + 1) * hd], wk, cos, sin) for h in range(heads)])
-    V = np.stack([C[:, 2 * d + h * hd:2 * d + (h + 1) * hd] for h in range(heads)])
+    K = np.stack([rms_rope(C[:, dq + h * hd:dq + (h + 1) * hd], wk, cos, sin) for h in range(hkv)])
+    V = np.stack([C[:, dq + dk + h * hd:dq + dk + (h + 1) * hd] for h in range(hkv)])
     return Q, K, V
 
 
@@ -108,18 +111,20 @@ def quantize_qkv(Q, K, V):
 
 
 def tiles(Q, K, V):
-    """(heads, M, 128) values before quantization -> the byte tiles q (heads, T, 9216), kv (heads, T, 2, 9216), each
-    tile encoded once from its float32 values (encoding already-quantized values again is not the identity in the
-    -128 corner)."""
+    """(heads, M, 128) values before quantization (K, V: kv heads) -> the byte tiles q (heads, T, 9216), kv (kv heads,
+    T, 2, 9216), each tile encoded once from its float32 values (encoding already-quantized values again is not the
+    identity in the -128 corner)."""
     Q, K, V = (np.asarray(a, np.float32) for a in (Q, K, V))
     H, M, _ = Q.shape
+    HKV = K.shape[0]
     T = M // TILE_TOKENS
     q = np.empty((H, T, 9216), np.uint8)
-    kv = np.empty((H, T, 2, 9216), np.uint8)
-    for h in range(H):
-        for t in range(T):
-            r = slice(t * TILE_TOKENS, (t + 1) * TILE_TOKENS)
+    kv = np.empty((HKV, T, 2, 9216), np.uint8)
+    for t in range(T):
+        r = slice(t * TILE_TOKENS, (t + 1) * TILE_TOKENS)
+        for h in range(H):
             q[h, t] = F.to_bfp16(F.a_layout(Q[h, r], 64, 128))
+        for h in range(HKV):
             kv[h, t, 0] = F.to_bfp16(F.b_layout(np.ascontiguousarray(K[h, r].T), 128, 64))
             kv[h, t, 1] = F.to_bfp16(F.b_layout(V[h, r], 64, 128))
     return q, kv

@@ -160,16 +160,19 @@ int rl_validate_ln(int64_t ldx, int32_t br_fmt, int64_t ld_br, int32_t norm, int
   return rl::ok();
 }
 
-int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads) {
+int rl_validate_qkv_post_gqa(int64_t ldc, int64_t M, int32_t hq, int32_t hkv) {
   using rl::fail;
-  if (heads < 1 || heads > 1024) return fail(RL_ERR_SHAPE, "heads %d: need 1..1024", heads);
+  if (hq < 1 || hq > 1024 || hkv < 1 || hkv > 1024)
+    return fail(RL_ERR_SHAPE, "heads %d / %d: need 1..1024 each", hq, hkv);
   if (M < 64 || M % 64 || M > (1 << 30))
     return fail(RL_ERR_SHAPE, "M %lld: need a positive multiple of 64", (long long)M);
-  if (M / 64 * heads * 3 > ((int64_t)1 << 31) - 1) return fail(RL_ERR_SHAPE, "more than 2^31 tiles");
-  if (ldc < 3 * 128 * (int64_t)heads || ldc % 8)
-    return fail(RL_ERR_ALIGN, "ldc %lld: need >= 3 * 128 * heads and a multiple of 8", (long long)ldc);
+  if (M / 64 * (hq + 2 * (int64_t)hkv) > ((int64_t)1 << 31) - 1) return fail(RL_ERR_SHAPE, "more than 2^31 tiles");
+  if (ldc < 128 * ((int64_t)hq + 2 * hkv) || ldc % 8)
+    return fail(RL_ERR_ALIGN, "ldc %lld: need >= 128 * (hq + 2 hkv) and a multiple of 8", (long long)ldc);
   return rl::ok();
 }
+
+int rl_validate_qkv_post(int64_t ldc, int64_t M, int32_t heads) { return rl_validate_qkv_post_gqa(ldc, M, heads, heads); }
 
 int rl_validate_attention(int32_t heads, int64_t nq, int64_t nk, int64_t nkv, int64_t ldo, int32_t h0) {
   using rl::fail;

@@ -95,7 +95,7 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
 
 // Re-quantize one block of 8 bf16 values (4 packed words) to bfp16, returned as bf16 words: the encoder's float fast
 // path (encode_fast / decode_fast: one exact power-of-two scaling and one half-to-even rounding per value) for block
-// exponents 7..237, the integer encoder otherwise, so the result equals the integer encoder's and does not depend on
+// exponents 8..237, the integer encoder otherwise, so the result equals the integer encoder's and does not depend on
 // the denormal mode. -0 comes back as +0, as from_bfp16 gives it.
 __device__ __forceinline__ u32x4 requantize8(u32x4 o) {
   const uint32_t w[4] = {o.x, o.y, o.z, o.w};
@@ -1094,6 +1094,10 @@ static int launch(const GemmArgs<G>& args, int total_tiles, int32_t a_fmt, void*
   return launch_status("rl_bfp16_gemm");
 }
 
+// Bytes of the bf16 A copy that rl_bfp16_gemm_ws stages at the start of the workspace for a non-bf16 A format,
+// rounded up so that the K-split partials after it stay 256-byte aligned.
+static int64_t staged_a_bytes(int64_t M, int64_t K) { return (M * K * 2 + 255) / 256 * 256; }
+
 }  // namespace rl
 
 extern "C" {
@@ -1106,6 +1110,16 @@ int64_t rl_bfp16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return plan_split(M, N, K, device_cus()).ws_bytes;
 }
 
+int64_t rl_bfp16_gemm_workspace_size(int32_t a_fmt, int64_t M, int64_t N, int64_t K) {
+  using namespace rl;
+  if (rl_validate_gemm(a_fmt, a_fmt == RL_A_BF16 || a_fmt == RL_A_BF16_QUANTIZE ? K : 0, N, M, N, K, nullptr))
+    return -1;
+  check_device();
+  ok();
+  const int64_t split = plan_split(M, N, K, device_cus()).ws_bytes;
+  return a_fmt == RL_A_BF16 ? split : staged_a_bytes(M, K) + split;
+}
+
 int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
                      int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* workspace, int64_t workspace_bytes,
                      void* stream) {
@@ -1116,7 +1130,26 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
   if ((uintptr_t)workspace % 16) return fail(RL_ERR_ALIGN, "the workspace must be 16-byte aligned");
   args.n = 1;
   if ((s = check_device())) return s;
-  if (a_fmt != RL_A_BF16) return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
+  if (a_fmt != RL_A_BF16) {
+    if (!workspace) return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
+    // stage A as bf16 (its bfp16 values) at the start of the workspace in one HBM-bound pass, then run the bf16
+    // path with the rest of the workspace
+    const int64_t sa = staged_a_bytes(M, K);
+    if (workspace_bytes < sa)
+      return fail(RL_ERR_WORKSPACE, "workspace %lld bytes, staging A needs %lld (rl_bfp16_gemm_workspace_size)",
+                  (long long)workspace_bytes, (long long)sa);
+    uint16_t* a16 = static_cast<uint16_t*>(workspace);
+    if (a_fmt == RL_A_BF16_QUANTIZE)
+      s = rl_bfp16_quantize(A, RL_DTYPE_BF16, M, K, lda, RL_ORDER_ROWBLOCK, nullptr, a16, stream);
+    else
+      s = rl_bfp16_dequantize(static_cast<const uint8_t*>(A),
+                              a_fmt == RL_A_PACKED_A_LAYOUT ? RL_ORDER_A_LAYOUT : RL_ORDER_ROWBLOCK, M, K, a16,
+                              RL_DTYPE_BF16, stream);
+    if (s) return s;
+    const int64_t rest = workspace_bytes - sa;
+    return rl_bfp16_gemm_ws(a16, RL_A_BF16, K, B_packed, C, ldc, M, N, K, ep,
+                            rest > 0 ? static_cast<uint8_t*>(workspace) + sa : nullptr, rest, stream);
+  }
   int total = 0;
   if (workspace) {
     const SplitPlan sp = plan_split(M, N, K, device_cus());

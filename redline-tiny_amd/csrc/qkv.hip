@@ -28,7 +28,7 @@ struct QkvArgs {
   const uint16_t* C;
   int64_t ldc;
   int64_t M;
-  int32_t heads;
+  int32_t hq, hkv;  // q heads, k / v heads (equal for the DiT; grouped-query attention has hq a multiple of hkv)
   const uint16_t* cos;
   const uint16_t* sin;
   const uint16_t* wq;
@@ -73,12 +73,22 @@ template <bool TILES, bool NATIVE>
 __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stage[kTile9];
   const int tid = threadIdx.x;
-  // workgroup = (part, head, tile): the three parts of one (head, tile) are neighbours in launch order
-  const int part = blockIdx.x % 3, ht = blockIdx.x / 3;
-  const int h = ht % a.heads, t = ht / a.heads;
+  // workgroup = (part, head) item j of 64-token tile t; C's columns are [q hq x 128 | k hkv x 128 | v hkv x 128].
+  // With hq == hkv the three parts of one (head, tile) are neighbours in launch order (j = 3 h + part); otherwise
+  // the q heads come first, then k and v head g side by side.
+  const int per_tile = a.hq + 2 * a.hkv;
+  const int t = blockIdx.x / per_tile, j = blockIdx.x - t * per_tile;
+  int part, h;
+  if (a.hq == a.hkv) {
+    part = j % 3; h = j / 3;
+  } else if (j < a.hq) {
+    part = 0; h = j;
+  } else {
+    part = 1 + ((j - a.hq) & 1); h = (j - a.hq) >> 1;
+  }
   const int64_t row0 = (int64_t)t * kTileTokens;
-  const int64_t D = (int64_t)a.heads * kHeadDim;
-  const int64_t col0 = part * D + h * kHeadDim;
+  const int64_t col0 = (part == 0 ? 0 : (int64_t)a.hq * kHeadDim + (part - 1) * (int64_t)a.hkv * kHeadDim) +
+                       (int64_t)h * kHeadDim;
   const bool tiles = TILES && (part == 0 ? a.q_tiles != nullptr : a.kv_tiles != nullptr);
 
   if (part < 2) {
@@ -147,11 +157,12 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
 
 }  // namespace rl
 
-extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t heads, const uint16_t* cos,
-                           const uint16_t* sin, const uint16_t* wq, const uint16_t* wk, uint8_t* q_tiles,
-                           uint8_t* kv_tiles, uint16_t* q, uint16_t* k, uint16_t* v, void* stream) {
+extern "C" int rl_qkv_post_gqa(const uint16_t* C, int64_t ldc, int64_t M, int32_t hq, int32_t hkv,
+                               const uint16_t* cos, const uint16_t* sin, const uint16_t* wq, const uint16_t* wk,
+                               uint8_t* q_tiles, uint8_t* kv_tiles, uint16_t* q, uint16_t* k, uint16_t* v,
+                               void* stream) {
   using namespace rl;
-  int s = rl_validate_qkv_post(ldc, M, heads);
+  int s = rl_validate_qkv_post_gqa(ldc, M, hq, hkv);
   if (s) return s;
   if (!C || !cos || !sin || !wq || !wk) return fail(RL_ERR_NULL, "C, cos, sin, wq or wk is NULL");
   if (!q_tiles && !kv_tiles && !q && !k && !v) return fail(RL_ERR_NULL, "every output is NULL");
@@ -162,10 +173,10 @@ extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t he
   if (((uintptr_t)cos | (uintptr_t)sin) % 8) return fail(RL_ERR_ALIGN, "cos / sin must be 8-byte aligned");
   if ((s = check_device())) return s;
   QkvArgs a;
-  a.C = C; a.ldc = ldc; a.M = M; a.heads = heads;
+  a.C = C; a.ldc = ldc; a.M = M; a.hq = hq; a.hkv = hkv;
   a.cos = cos; a.sin = sin; a.wq = wq; a.wk = wk;
   a.q_tiles = q_tiles; a.kv_tiles = kv_tiles; a.q = q; a.k = k; a.v = v;
-  const dim3 grid((unsigned)(M / kTileTokens * heads * 3));
+  const dim3 grid((unsigned)(M / kTileTokens * (hq + 2 * hkv)));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const bool tiles = q_tiles || kv_tiles, native = q || k || v;
   if (tiles && native)
@@ -175,4 +186,10 @@ extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t he
   else
     hipLaunchKernelGGL((qkv_post_kernel<false, true>), grid, dim3(kQkvThreads), 0, st, a);
   return launch_status("rl_qkv_post");
+}
+
+extern "C" int rl_qkv_post(const uint16_t* C, int64_t ldc, int64_t M, int32_t heads, const uint16_t* cos,
+                           const uint16_t* sin, const uint16_t* wq, const uint16_t* wk, uint8_t* q_tiles,
+                           uint8_t* kv_tiles, uint16_t* q, uint16_t* k, uint16_t* v, void* stream) {
+  return rl_qkv_post_gqa(C, ldc, M, heads, heads, cos, sin, wq, wk, q_tiles, kv_tiles, q, k, v, stream);
 }

@@ -150,15 +150,18 @@ __device__ __forceinline__ u32x4 quantize_bf16x8(u32x4 v, uint32_t* E_out = null
   return r;
 }
 
-// Float fast path of the encoder for a block exponent E in 7..237 (kFastEMin..kFastEMax). With s = 2^(133-E) and t = 127 * 2^(E-133):
+// Float fast path of the encoder for a block exponent E in 8..237 (kFastEMin..kFastEMax). With s = 2^(133-E) and t = 127 * 2^(E-133):
 // fma(min(x, t), s, 1.5 * 2^23) scales exactly (a power of two) and rounds once, half to even, at integer
 // granularity, because the 1.5 * 2^23 term is even and |x * s| < 2^22. The result's bits are 0x4B400000 + q, so the
 // low byte is q in two's complement; min(x, t) clips q at 127, and q >= -128 holds by the choice of E. Values too small
 // to reach 0.5 after scaling round to 0, as the integer encoder gives. (f - 1.5 * 2^23) * 2^(E-133) is the decoded
 // value, exactly, and a normal float. Above E = 237 the constant -1.5 * 2^23 * 2^(E-133) of decode_fast overflows
-// float32, so such blocks (values of 2^111 and more) take the integer encoder.
+// float32, so such blocks (values of 2^111 and more) take the integer encoder. From E = 8 up every float32 subnormal
+// element scales below 0.5 (x < 2^-126, s <= 2^125) and rounds to 0 whether or not the hardware flushes denormals, so
+// the fast path's result does not depend on the denormal mode; at E = 7 a subnormal in [2^-127, 2^-126) would scale
+// into [0.5, 1), so E <= 7 takes the integer encoder.
 constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23
-constexpr uint32_t kFastEMin = 7u, kFastEMax = 237u;
+constexpr uint32_t kFastEMin = 8u, kFastEMax = 237u;
 struct BlockScale {
   float s, t, inv;  // 2^(133-E), 127 * 2^(E-133), 2^(E-133)
 };
@@ -178,7 +181,7 @@ __device__ __forceinline__ uint32_t decode_fast_bits(float f, const BlockScale& 
 
 // Encode 8 float32 bit patterns (finite) to one block: returns E, writes q (the int8 value in the low byte of each
 // word: callers store the byte) and the decoded values as bf16, packed two per word (value 2i in the low half of word
-// i). The largest exponent field is that of the largest magnitude. For block exponents 7..237 the float fast path
+// i). The largest exponent field is that of the largest magnitude. For block exponents 8..237 the float fast path
 // above is used; other exponents (subnormal blocks, very large ones, and infinities, which saturate) take the integer
 // encoder.
 __device__ __forceinline__ uint32_t encode_block(const uint32_t u[8], int32_t q[8], u32x4& bw) {

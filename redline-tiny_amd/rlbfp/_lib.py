@@ -55,11 +55,13 @@ SIGNATURES = {
     "rl_bfp16_gemm_ws": (ctypes.c_int, [_P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue),
                                         _P, _I64, _P]),
     "rl_bfp16_gemm_workspace_bytes": (ctypes.c_int64, [_I64, _I64, _I64]),
+    "rl_bfp16_gemm_workspace_size": (ctypes.c_int64, [_I32, _I64, _I64, _I64]),
     "rl_bfp16_gemm_grouped": (ctypes.c_int, [ctypes.POINTER(GemmDesc), _I32, _I32, _P]),
     "rl_bfp16_gemv": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "rl_ln_modulate": (ctypes.c_int, [_P, _I64, _P, _I32, _I64, _P, _I64, _I32, _P, _I64, _P, _I32, _P, _I64, _I64,
                                       _I64, _P]),
     "rl_qkv_post": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "rl_qkv_post_gqa": (ctypes.c_int, [_P, _I64, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "rl_attention": (ctypes.c_int, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _P, _I64, _I32, _I32, _P]),
     "rl_attention_ws": (ctypes.c_int, [_P, _P, _P, _I32, _I64, _I64, _I64, _P, _P, _I64, _I32, _I32, _P, _I64, _P]),
     "rl_attention_workspace_bytes": (ctypes.c_int64, [_I32, _I64, _I64]),
@@ -68,6 +70,7 @@ SIGNATURES = {
     "rl_validate_gemv": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I32]),
     "rl_validate_ln": (ctypes.c_int, [_I64, _I32, _I64, _I32, _I64, _I32, _I64, _I64, _I64, _I64]),
     "rl_validate_qkv_post": (ctypes.c_int, [_I64, _I64, _I32]),
+    "rl_validate_qkv_post_gqa": (ctypes.c_int, [_I64, _I64, _I32, _I32]),
     "rl_validate_attention": (ctypes.c_int, [_I32, _I64, _I64, _I64, _I64, _I32]),
     "rl_packed_bytes": (ctypes.c_int64, [_I64, _I64]),
     "rl_last_error": (ctypes.c_char_p, []),

@@ -137,22 +137,30 @@ def _a_args(a, a_fmt, M, K):
 _GEMM_WS = {}
 
 
-def gemm_workspace_bytes(M, N, K, device=None):
-    """Bytes of the K-split workspace of an RL_A_BF16 GEMM of this shape (0: it runs whole); cached per shape."""
-    key = (M, N, K, torch.cuda.current_device() if device is None else torch.device(device).index)
+def gemm_workspace_bytes(M, N, K, device=None, a_fmt="bf16"):
+    """Bytes of rl_bfp16_gemm_ws's workspace for this shape and A format: the K-split partials (0: the shape runs
+    whole), plus the staged bf16 copy of A for a non-bf16 format; cached per shape."""
+    key = (M, N, K, a_fmt, torch.cuda.current_device() if device is None else torch.device(device).index)
     if key not in _GEMM_WS:
-        n = L.lib().rl_bfp16_gemm_workspace_bytes(M, N, K)
+        n = L.lib().rl_bfp16_gemm_workspace_size(A_FORMATS[a_fmt], M, N, K)
         if n < 0:
-            raise ValueError(f"invalid GEMM shape M={M} N={N} K={K}")
+            raise ValueError(f"invalid GEMM shape M={M} N={N} K={K} for A format {a_fmt}")
         _GEMM_WS[key] = n
     return _GEMM_WS[key]
 
 
+def staged_a_bytes(M, K):
+    """Bytes of the bf16 A copy rl_bfp16_gemm_ws stages for a non-bf16 A format (rounded up to 256)."""
+    return (M * K * 2 + 255) // 256 * 256
+
+
 def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None, gate_split_row=0,
-         residual=None, quantize_out=False, out=None, split=True):
+         residual=None, quantize_out=False, out=None, split=True, stage=True):
     """C = epilogue(A @ B) with B the packed weight stream of a (K, N) matrix, bf16 output (M, N) (or (M, N/2) for
     act="swiglu"). See rl_bfp16_gemm in include/rlbfp.h for the epilogue order. split: let a small-M, deep-K GEMM
-    split K into pieces (rl_bfp16_gemm_ws, workspace from torch's allocator); False: always the whole-K kernel."""
+    split K into pieces (rl_bfp16_gemm_ws, workspace from torch's allocator); False: always whole K. stage: for an
+    A format other than "bf16", decode (or quantize) A into a bf16 copy in the workspace first and run the bf16
+    kernel; False: the register-staged kernel reads the format directly (slower)."""
     _dev(a, "A")
     _dev(b_packed, "B")
     if M is None:
@@ -169,7 +177,12 @@ def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None
         raise ValueError(f"out must be ({M}, {nout}) bfloat16 with unit column stride")
     _check_ep_sizes(M, N, nout, bias, gate, gate_split_row, residual)
     ep = _epilogue(act, bias, gate, gate_split_row, residual, quantize_out)
-    nws = gemm_workspace_bytes(M, N, K, a.device) if split and a_fmt == "bf16" else 0
+    if a_fmt == "bf16":
+        nws = gemm_workspace_bytes(M, N, K, a.device) if split else 0
+    elif stage:
+        nws = gemm_workspace_bytes(M, N, K, a.device, a_fmt) if split else staged_a_bytes(M, K)
+    else:
+        nws = 0
     if nws:
         ws = torch.empty(nws, dtype=torch.uint8, device=a.device)
         L.check(L.lib().rl_bfp16_gemm_ws(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M,
@@ -287,31 +300,43 @@ def ln_modulate(x, params, branch=None, split_row=0, norm="layer", x_out=None, p
 # QKV post -> attention Q / K / V
 # ---------------------------------------------------------------------------------------------------------------
 
-def qkv_post(C, cos, sin, wq, wk, heads, tiles=True, native=False):
+def qkv_post(C, cos, sin, wq, wk, heads, tiles=True, native=False, kv_heads=None, out_tiles=None):
     """Per head of 128 dims: Q = rope(rms(q) * wq), K = rope(rms(k) * wk), V = v, quantized to bfp16 (Q, K in blocks
-    of 8 dims, V in blocks of 8 tokens). C (M, 3 * heads * 128) bf16; cos, sin (M, 64) bf16; wq, wk (128,) bf16.
-    Returns (q_tiles (heads, M/64, 9216) uint8, kv_tiles (heads, M/64, 2, 9216) uint8) if tiles, else None, None;
-    then, if native, q and k (heads, M, 128) and v transposed, (heads, 128, M), bf16, else None x 3. See rl_qkv_post
-    in include/rlbfp.h."""
+    of 8 dims, V in blocks of 8 tokens). C (M, (heads + 2 * kv_heads) * 128) bf16 (kv_heads None: = heads; fewer for
+    grouped-query attention); cos, sin (M, 64) bf16; wq, wk (128,) bf16.
+    Returns (q_tiles (heads, M/64, 9216) uint8, kv_tiles (kv_heads, M/64, 2, 9216) uint8) if tiles, else None, None;
+    then, if native, q (heads, M, 128), k (kv_heads, M, 128) and v transposed, (kv_heads, 128, M), bf16, else
+    None x 3. out_tiles: a (q_tiles, kv_tiles) pair of caller-owned uint8 tensors of those sizes to write instead.
+    See rl_qkv_post_gqa in include/rlbfp.h."""
     for t, n in ((C, "C"), (cos, "cos"), (sin, "sin"), (wq, "wq"), (wk, "wk")):
         _dev(t, n)
         if t.dtype != torch.bfloat16:
             raise ValueError(f"{n} must be bfloat16")
+    hkv = heads if kv_heads is None else kv_heads
     M = C.shape[0]
-    if C.dim() != 2 or C.stride(1) != 1 or C.shape[1] != 3 * 128 * heads:
-        raise ValueError(f"C must be (M, {3 * 128 * heads}) with unit column stride")
+    if C.dim() != 2 or C.stride(1) != 1 or C.shape[1] != 128 * (heads + 2 * hkv):
+        raise ValueError(f"C must be (M, {128 * (heads + 2 * hkv)}) with unit column stride")
     if cos.shape != (M, 64) or sin.shape != (M, 64) or not cos.is_contiguous() or not sin.is_contiguous():
         raise ValueError("cos and sin must be contiguous (M, 64)")
     if wq.numel() != 128 or wk.numel() != 128 or not wq.is_contiguous() or not wk.is_contiguous():
         raise ValueError("wq and wk must be contiguous 128-vectors")
     T = M // 64
-    qt = torch.empty((heads, T, 9216), dtype=torch.uint8, device=C.device) if tiles else None
-    kvt = torch.empty((heads, T, 2, 9216), dtype=torch.uint8, device=C.device) if tiles else None
+    if out_tiles is not None:
+        qt, kvt = out_tiles
+        for t, n, want in ((qt, "q tiles", heads * T * 9216), (kvt, "kv tiles", hkv * T * 2 * 9216)):
+            _dev(t, n)
+            if t.dtype != torch.uint8 or t.numel() != want or not t.is_contiguous():
+                raise ValueError(f"{n} must be a contiguous uint8 tensor of {want} bytes")
+    elif tiles:
+        qt = torch.empty((heads, T, 9216), dtype=torch.uint8, device=C.device)
+        kvt = torch.empty((hkv, T, 2, 9216), dtype=torch.uint8, device=C.device)
+    else:
+        qt = kvt = None
     q, k, v = ((torch.empty((heads, M, 128), dtype=torch.bfloat16, device=C.device),
-                torch.empty((heads, M, 128), dtype=torch.bfloat16, device=C.device),
-                torch.empty((heads, 128, M), dtype=torch.bfloat16, device=C.device)) if native else (None, None, None))
-    L.check(L.lib().rl_qkv_post(_ptr(C), C.stride(0), M, heads, _ptr(cos), _ptr(sin), _ptr(wq), _ptr(wk), _ptr(qt),
-                                _ptr(kvt), _ptr(q), _ptr(k), _ptr(v), _stream(C)))
+                torch.empty((hkv, M, 128), dtype=torch.bfloat16, device=C.device),
+                torch.empty((hkv, 128, M), dtype=torch.bfloat16, device=C.device)) if native else (None, None, None))
+    L.check(L.lib().rl_qkv_post_gqa(_ptr(C), C.stride(0), M, heads, hkv, _ptr(cos), _ptr(sin), _ptr(wq), _ptr(wk),
+                                    _ptr(qt), _ptr(kvt), _ptr(q), _ptr(k), _ptr(v), _stream(C)))
     return qt, kvt, q, k, v
 
 

@@ -109,3 +109,25 @@ def unpack_head(q, kv, h):
     K = torch.cat([layouts.b_unlayout(kv[h, t, 0], 128, 64, 128, 64).t() for t in range(T)])
     V = torch.cat([layouts.b_unlayout(kv[h, t, 1], 64, 128, 64, 128) for t in range(T)])
     return Q, K, V
+
+
+def qkv_post_run(art, cin, tabs, q_out, kv_out):
+    """NPU.run("qkv_post", art, [C, TABS, Q, KV]): the QKV-post artifacts' buffer contract (redline/forward.py:246,
+    :368; GQA copy: redline/vlm_run.py:433-437, kernels/vlm/qkv_gqa_design.py:1-10), written into the caller's Q
+    (heads, T, 9216) and KV (kv heads, T, 2, 9216) uint8 buffers. C is the QKV GEMM's output: bfp16 in the C-stream
+    order c_layout_atb(., 128, 128) (uint8), bf16 in that order (a flat bf16 tensor, the C16 GEMMs'), or the build's
+    native (M, N) bf16. TABS: the qkv_tables buffer (T, 8448) bf16. The head counts follow from the buffer sizes;
+    `art` is accepted for the reference's signature."""
+    T = tabs.numel() // TAB
+    M = 64 * T
+    hq, hkv = q_out.numel() // (T * 9216), kv_out.numel() // (T * 2 * 9216)
+    n_cols = 128 * (hq + 2 * hkv)
+    if cin.dtype == torch.uint8:
+        C = ops.dequantize(cin.reshape(-1), M, n_cols, order="c_atb", dtype=torch.bfloat16)
+    elif cin.dim() == 1:
+        C = layouts.c_unlayout_atb_values(cin, M, n_cols)
+    else:
+        C = cin
+    cos, sin, wqc, wk = tables_rows(tabs.reshape(T, TAB))
+    ops.qkv_post(C, cos.contiguous(), sin.contiguous(), wqc, wk, hq, kv_heads=hkv,
+                 out_tiles=(q_out.reshape(-1), kv_out.reshape(-1)))

@@ -191,3 +191,33 @@ def _has_gpu():
         return torch.cuda.device_count() > 0
     except Exception:
         return False
+
+
+def test_gemm_workspace_size_per_a_format():
+    """rl_bfp16_gemm_workspace_size: the K-split partials for RL_A_BF16; for the other A formats also the staged bf16
+    copy of A, M * K * 2 rounded up to 256 bytes; -1 for an invalid shape or format."""
+    size, split = L.lib().rl_bfp16_gemm_workspace_size, L.lib().rl_bfp16_gemm_workspace_bytes
+    for M, N, K in ((4352, 24576, 3072), (512, 4096, 12288), (100, 384, 4096), (1, 128, 64)):
+        assert size(L.RL_A_BF16, M, N, K) == split(M, N, K)
+        for fmt in (L.RL_A_BF16_QUANTIZE, L.RL_A_PACKED_ROWBLOCK):
+            assert size(fmt, M, N, K) == (M * K * 2 + 255) // 256 * 256 + split(M, N, K)
+    assert size(L.RL_A_PACKED_A_LAYOUT, 4096, 3072, 3072) == 4096 * 3072 * 2
+    assert size(L.RL_A_PACKED_A_LAYOUT, 100, 384, 4096) == -1   # the A layout needs M % 128 == 0
+    assert size(7, 128, 128, 64) == -1
+    assert size(L.RL_A_BF16, 128, 100, 64) == -1
+
+
+@pytest.mark.parametrize("args,code", [
+    ((6144, 1536, 32, 8), L.RL_OK),
+    ((9216, 4352, 24, 24), L.RL_OK),
+    ((6144 - 8, 1536, 32, 8), L.RL_ERR_ALIGN),
+    ((6144, 1536, 32, 0), L.RL_ERR_SHAPE),
+    ((6144, 1500, 32, 8), L.RL_ERR_SHAPE),
+])
+def test_validate_qkv_post_gqa(args, code):
+    assert L.lib().rl_validate_qkv_post_gqa(*args) == code
+
+
+def test_qkv_post_gqa_null_pointers_rejected_before_any_gpu_call():
+    assert L.lib().rl_qkv_post_gqa(None, 6144, 64, 32, 8, None, None, None, None, None, None, None, None, None,
+                                   None) == L.RL_ERR_NULL

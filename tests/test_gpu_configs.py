@@ -125,3 +125,59 @@ def test_config5_grouped_streams(dev):
     wm, Bm = packed_weight(rng, 6 * K, K)
     y = ops.gemv(cuda(temb, torch.bfloat16), wm, 6 * K, act="silu")
     assert G.rel_err(y.float().cpu().numpy(), G.gemv_ref(temb, Bm)) <= TOL
+
+
+@pytest.mark.parametrize("op", ["out_proj", "up_swiglu", "down"])
+def test_config5_grouped_launches(dev, op):
+    """Config 5's other grouped launches at full size, image (M=4096) and text (M=256) streams with separate weights:
+    the out-projection (K = N = 3072), the SwiGLU up GEMM with re-quantized H (K = 3072, N = 2 x 12288) and the down
+    GEMM (K = 12288, N = 3072), each checked on sampled rows against the emulation and bit-identical to single
+    launches."""
+    rng = np.random.default_rng({"out_proj": 1, "up_swiglu": 2, "down": 3}[op])
+    K, FF = 3072, 12288
+    Kop, N = {"out_proj": (K, K), "up_swiglu": (K, 2 * FF), "down": (FF, K)}[op]
+    kind = "swiglu" if op == "up_swiglu" else None
+    streams = []
+    for M in (4096, 256):
+        A = G.activations(rng, M, Kop)
+        bw, Bq = packed_up(rng, FF, K) if kind else packed_weight(rng, N, Kop)
+        _, aq = ops.quantize(cuda(A, torch.bfloat16), deq=True)
+        streams.append((M, A, bw, Bq, aq))
+    specs = [ops.GemmSpec(aq, bw, N, Kop, act=kind, quantize_out=kind is not None) for (_, _, bw, _, aq) in streams]
+    outs = ops.gemm_grouped(specs)
+    for (M, A, bw, Bq, aq), o in zip(streams, outs):
+        assert torch.equal(o, ops.gemm(aq, bw, N, Kop, act=kind, quantize_out=kind is not None, split=False))
+        rows = sample_rows(rng, M, n=16)
+        ref = G.gemm_ref(F.quantize_rows(A[rows]), Bq, act=G.ACT_SWIGLU if kind else G.ACT_NONE,
+                         quantize_out=kind is not None)
+        check_rows(o, rows, ref)
+
+
+def test_packer_full_size_against_c_restatement(dev):
+    """The GPU weight packer at config 3's up-projection size (W_up 2 x 12288 x 3072 interleaved, 84.9 MB packed)
+    against the oracle's integer C encoder applied to the b_layout of B = W.T, compared 2048 columns (16 N tiles) at a
+    time: every byte equal."""
+    from oracle import bfp16_c as C
+    rng = np.random.default_rng(0)
+    K, FF = 3072, 12288
+    wg, wp = G.linear_weight(rng, FF, K), G.linear_weight(rng, FF, K)
+    W = F.interleave_up(wg, wp).T.copy()          # the Linear weight (2 FF, K) whose B = W.T is interleave_up's
+    got = ops.pack_weight(cuda(W, torch.float32)).cpu().numpy()
+    per = K * 2048 // 8 * 9                        # bytes of 2048 columns: N tiles are contiguous in the stream
+    for c0 in range(0, 2 * FF, 2048):
+        want = C.to_bfp16(F.b_layout(np.ascontiguousarray(W[c0:c0 + 2048].T)))
+        np.testing.assert_array_equal(got[c0 // 2048 * per:(c0 // 2048 + 1) * per], want)
+
+
+def test_gemv_against_unquantized_reference_math(dev):
+    """The modulation GEMV at config 5's size against the reference's own math, linear(silu(te), W) with an
+    unquantized activation in float64 (redline/host_glue.py:26-28, :43-44) on the packed weights' values: the
+    activation encoding the GPU applies (bfp16 blocks of 8) stays within the 1e-2 bar."""
+    rng = np.random.default_rng(5)
+    K, N = 3072, 18432
+    temb = F.bf16_round(rng.standard_normal((1, K)).astype(np.float32))
+    wm, Bm = packed_weight(rng, N, K)
+    y = ops.gemv(cuda(temb, torch.bfloat16), wm, N, act="silu").float().cpu().numpy()
+    ref = G.silu(temb.astype(np.float64)) @ Bm.astype(np.float64)
+    assert G.rel_err(y, ref) <= TOL
+    assert G.corr(y, ref) > 0.999

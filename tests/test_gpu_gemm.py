@@ -59,9 +59,11 @@ def test_output_canary_and_ldc(dev):
     assert (big[:, N:] == 7.0).all() and (big[M:, :] == 7.0).all()
 
 
+@pytest.mark.parametrize("stage", [True, False])
 @pytest.mark.parametrize("a_fmt", ["bf16_quantize", "packed_rowblock", "packed_a_layout"])
-def test_a_formats_agree(dev, a_fmt):
-    """Every A format computes on the same bfp16 values: results identical to the bf16 (pre-quantized) path."""
+def test_a_formats_agree(dev, a_fmt, stage):
+    """Every A format computes on the same bfp16 values: results identical to the bf16 (pre-quantized) path, whether A
+    is staged as bf16 in the workspace first (stage) or read by the register-staged kernel."""
     M, K, N = 256, 192, 256
     rng, A, packed, Aq, Bq = setup(M, K, N, 4, outliers=0.01)
     b = dev_t(packed, torch.uint8)
@@ -72,7 +74,7 @@ def test_a_formats_agree(dev, a_fmt):
         a = dev_t(F.to_bfp16(A.reshape(-1)), torch.uint8)
     else:
         a = dev_t(F.to_bfp16(F.a_layout(A)), torch.uint8)
-    got = ops.gemm(a, b, N, K, M=M, a_fmt=a_fmt)
+    got = ops.gemm(a, b, N, K, M=M, a_fmt=a_fmt, stage=stage)
     assert torch.equal(got, ref)
     check(got, G.gemm_ref(Aq, Bq))
 
@@ -131,6 +133,27 @@ def test_quantize_out(dev):
     q_new = raw.reshape(-1, 9)[:, 1:].view(np.int8)[np.arange(len(blocks)), i]
     assert same[~corner].all()
     assert (q_new[~same] == -64).all()
+
+
+def test_requantize_exponent_bounds(dev):
+    """The epilogue's re-quantize on blocks at and around the float fast path's bounds (block exponents 7/8 and
+    237/238), with bf16 subnormal elements beside an E = 7 maximum: gate 0 makes the output the residual itself, so
+    the result must equal the encoder's blocks of the residual exactly."""
+    M, K, N = 128, 64, 128
+    rng, A, packed, Aq, Bq = setup(M, K, N, 21)
+    rows = []
+    for e in (1, 6, 7, 8, 9, 120, 236, 237, 238, 250):
+        step = 2.0 ** (e - 133)
+        rows.append((rng.integers(-127, 127, 8) + 0.5) * step)
+        rows.append(np.array([127.5, -127.5, 64.5, -64.5, 0.5, -0.5, 1.5, -2.5]) * step)
+    for e in (7, 8):
+        rows.append(np.array([1.5 * 2.0 ** (e - 127), 2**-127, -2**-127, 1.5 * 2**-127, -1.5 * 2**-127,
+                              1.75 * 2**-127, 2**-128, -1.5 * 2**-128]))
+    blocks = F.bf16_round(np.concatenate(rows).astype(np.float32).reshape(-1, 8))
+    res = np.tile(blocks, (M * N // 8 // len(blocks) + 1, 1))[: M * N // 8].reshape(M, N)
+    out = ops.gemm(dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8), N, K, gate=dev_t(np.zeros(N), torch.float32),
+                   residual=dev_t(res, torch.bfloat16), quantize_out=True)
+    np.testing.assert_array_equal(out.float().cpu().numpy(), F.quantize_rows(res))
 
 
 def test_grouped_matches_single(dev):

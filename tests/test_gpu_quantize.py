@@ -58,24 +58,34 @@ def test_orders_bit_exact(dev, order, R, Cc, dtype):
     np.testing.assert_array_equal(back.cpu().numpy(), F.quantize_rows(x))
 
 
-def test_adversarial_blocks(dev):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_adversarial_blocks(dev, dtype):
     """ties at every exponent, saturation, -128, zeros, float32 subnormals, signed zeros, infinities. Block exponents
-    6/7 and 237/238 bound the kernels' float fast path (7..237); the others take the integer encoder."""
+    7/8 and 237/238 bound the kernels' float fast path (8..237); the others take the integer encoder. E = 7 blocks
+    hold subnormal elements in [2^-127, 2^-126), which scale into [0.5, 1): 2^-127 is a tie (q = 0), 1.5 * 2^-127
+    gives q = 1 (the answer with IEEE denormals, which the integer encoder computes)."""
     rng = np.random.default_rng(11)
     rows = []
-    for e in sorted(set(range(1, 255, 3)) | {6, 7, 236, 237, 238, 254}):
+    for e in sorted(set(range(1, 255, 3)) | {6, 7, 8, 236, 237, 238, 254}):
         step = 2.0 ** (e - 133)
         rows.append((rng.integers(-127, 127, 8) + 0.5) * step)
         rows.append(np.array([127.5, -127.5, 64.5, -64.5, 0.5, -0.5, 1.5, -2.5]) * step)
     rows.append(rng.integers(-2**23 + 1, 2**23, 8) * 2.0 ** -149)      # subnormal block (E = 0)
     rows.append(np.array([2**-149, -2**-149, 0, -0.0, 2**-140, 0, 0, 0]))
+    for e in (7, 8):                                                    # subnormal elements beside an E = 7 / 8 max
+        rows.append(np.array([1.5 * 2.0 ** (e - 127), 2**-127, -2**-127, 1.5 * 2**-127, -1.5 * 2**-127,
+                              1.75 * 2**-127, 2**-128, -1.5 * 2**-128]))
     rows.append(np.array([np.inf, -np.inf, 1.0, 0, 0, 0, 0, 0]))        # E = 255, saturates
     x = np.concatenate(rows).astype(np.float32).reshape(-1, 8)
-    p, q = ops.quantize(to_dev(x), deq=True)
+    if dtype == torch.bfloat16:
+        x = F.bf16_round(x)
+    p, q = ops.quantize(to_dev(x, dtype), deq=True)
     np.testing.assert_array_equal(p.cpu().numpy(), C.to_bfp16(x))
     np.testing.assert_array_equal(p.cpu().numpy(), F.to_bfp16(x))
     fin = np.isfinite(x).all(1)
     np.testing.assert_array_equal(q.float().cpu().numpy()[fin], F.quantize_rows(x)[fin])
+    e7 = F.to_bfp16(x[-3:-2]).reshape(9)                                # the E = 7 row: q = [96, 0, 0, 1, -1, 1, 0, 0]
+    assert e7[0] == 7 and list(e7[1:].view(np.int8)) == [96, 0, 0, 1, -1, 1, 0, 0]
 
 
 def test_truncate_variant_differs(dev):

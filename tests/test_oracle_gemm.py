@@ -80,3 +80,61 @@ def test_gemv_matches_loop():
     want = F.bf16_round_f64(brute(a, Bq))
     np.testing.assert_array_equal(got, want)
     assert not np.array_equal(got, F.bf16_round_f64(brute(G.silu(x), Bq)))   # and that quantization matters
+
+
+# ---- silu / gelu_tanh pinned by library routines (torch's and scipy's float64 implementations) --------------------
+
+def _grid():
+    """|x| up to 30 (both exponential tails), a dense core, and the SwiGLU gate / GELU input range of the FFN shapes
+    (accumulators of K = 3072 products of N(0,1) activations and N(0, 0.02) weights: |v| < ~6)."""
+    rng = np.random.default_rng(7)
+    return np.concatenate([np.linspace(-30.0, 30.0, 6001), np.linspace(-6.0, 6.0, 4001),
+                           rng.standard_normal(4000) * 1.1, [0.0, -0.0, 1e-30, -1e-30, 5e-8]])
+
+
+def _pinned(f, ref, x):
+    """f agrees with the library routine to float64 rounding: 1e-13 absolute plus 1e-13 relative."""
+    got = np.asarray(f(x), np.float64)
+    return bool(np.all(np.abs(got - ref) <= 1e-13 + 1e-13 * np.abs(ref)))
+
+
+def _torch_ref(name, x):
+    import torch
+    t = torch.as_tensor(x, dtype=torch.float64)
+    if name == "silu":
+        return torch.nn.functional.silu(t).numpy()
+    return torch.nn.functional.gelu(t, approximate="tanh").numpy()
+
+
+def test_silu_matches_library_float64():
+    from scipy.special import expit
+    x = _grid()
+    assert _pinned(G.silu, _torch_ref("silu", x), x)
+    assert _pinned(G.silu, x * expit(x), x)
+
+
+def test_gelu_tanh_matches_library_float64():
+    x = _grid()
+    assert _pinned(G.gelu_tanh, _torch_ref("gelu_tanh", x), x)
+
+
+def test_activation_pins_reject_plausible_mistakes():
+    """Each mutant (a rounded constant, a sign, the erf form, a missing term) must fail the same check that the
+    oracle passes."""
+    from scipy.special import erf
+    x = _grid()
+    g_ref, s_ref = _torch_ref("gelu_tanh", x), _torch_ref("silu", x)
+
+    def gelu_c(c=0.044715, k=np.sqrt(2.0 / np.pi)):
+        return lambda v: 0.5 * v * (1.0 + np.tanh(k * (v + c * v ** 3)))
+
+    gelu_mutants = [gelu_c(c=0.0447), gelu_c(k=0.7978), gelu_c(k=np.sqrt(np.pi / 2.0)), gelu_c(c=0.0),
+                    lambda v: 0.5 * v * (1.0 + erf(v / np.sqrt(2.0))),
+                    lambda v: v / (1.0 + np.exp(-1.702 * v))]
+    for m in gelu_mutants:
+        assert not _pinned(m, g_ref, x)
+    silu_mutants = [lambda v: v / (1.0 + np.exp(v)), lambda v: 1.0 / (1.0 + np.exp(-v)),
+                    lambda v: v / (1.0 + np.exp2(-v)), lambda v: v / (1.0 + np.exp(-v.astype(np.float32)))]
+    for m in silu_mutants:
+        assert not _pinned(m, s_ref, x)
+    assert _pinned(gelu_c(), g_ref, x)   # the check itself accepts a faithful restatement

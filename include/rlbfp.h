@@ -124,6 +124,18 @@ int64_t rl_bfp16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * (M * K * 2 rounded up to 256), plus the K-split partials; -1: invalid shape or format. */
 int64_t rl_bfp16_gemm_workspace_size(int32_t a_fmt, int64_t M, int64_t N, int64_t K);
 
+/* rl_bfp16_gemm_ws without a workspace argument and without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no counterpart
+ * in the reference. The workspace is a fixed device array of RL_NOALLOC_SCRATCH_BYTES inside the library; each GPU
+ * the library runs on holds its own copy until the process ends. Shapes and A formats whose
+ * rl_bfp16_gemm_workspace_size() exceeds it are rejected with RL_ERR_WORKSPACE (64 MiB holds, e.g., the K-split
+ * partials of the text encoder's down projection at M = 512 and the staged A of up to 32M values). Results are those
+ * of rl_bfp16_gemm_ws with a workspace of that size. Every call on one GPU shares that GPU's array, and no byte of it
+ * is read before the same call wrote it: calls that overlap on one GPU (different streams or threads) race. */
+#define RL_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int rl_bfp16_gemm_noalloc(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
+                          int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *stream);
+
 /* Several independent GEMMs (different shapes, weights and epilogues, one A format) in one launch, e.g. the image-
  * and text-stream projections of a DiT block. At most RL_MAX_GROUP descriptors. Replaces the per-op sequence of
  * CachedStep.blocks (redline/forward.py:240-254) for GEMMs that do not depend on each other. */

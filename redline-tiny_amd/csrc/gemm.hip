@@ -20,6 +20,8 @@
 #include <math.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "rlbfp.h"
 #include "rlbfp_device.h"
 #include "rlbfp_host.h"
@@ -1185,6 +1187,60 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
 int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
                   int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* stream) {
   return rl_bfp16_gemm_ws(A, a_fmt, lda, B_packed, C, ldc, M, N, K, ep, nullptr, 0, stream);
+}
+
+}  // extern "C"
+
+// ---- the allocation-free variant: the workspace is a file-scope device array --------------------------------------
+// Each GPU that runs this code holds its own copy of `scratch` until the process ends. Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in symbol): the device address of this GPU's copy is
+// looked up once per device with hipGetSymbolAddress and kept in scratch_ptr[device].
+static __device__ __align__(256) uint8_t scratch[RL_NOALLOC_SCRATCH_BYTES];
+
+namespace rl {
+namespace {
+constexpr int kScratchDevices = 64;
+uint8_t* scratch_ptr[kScratchDevices] = {};
+std::mutex scratch_mu;
+
+// This device's address of `scratch` (the current device), looked up on its first use; RL_OK or RL_ERR_DEVICE.
+int scratch_for_current_device(uint8_t** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(RL_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kScratchDevices) return fail(RL_ERR_DEVICE, "device %d: at most %d devices", dev, kScratchDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(RL_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = scratch_ptr[dev];
+  return RL_OK;
+}
+}  // namespace
+}  // namespace rl
+
+extern "C" {
+
+int rl_bfp16_gemm_noalloc(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K, const rl_epilogue* ep, void* stream) {
+  using namespace rl;
+  int s = rl_validate_gemm(a_fmt, lda, ldc, M, N, K, ep);
+  if (s) return s;
+  if ((s = check_device())) return s;
+  const int64_t need = rl_bfp16_gemm_workspace_size(a_fmt, M, N, K);
+  if (need < 0) return fail(RL_ERR_SHAPE, "M %lld N %lld K %lld: invalid shape for A format %d", (long long)M,
+                            (long long)N, (long long)K, a_fmt);
+  if (need > RL_NOALLOC_SCRATCH_BYTES)
+    return fail(RL_ERR_WORKSPACE,
+                "M %lld N %lld K %lld (A format %d) needs %lld bytes of scratch, above the fixed %lld "
+                "(RL_NOALLOC_SCRATCH_BYTES); use rl_bfp16_gemm_ws with a workspace of that size",
+                (long long)M, (long long)N, (long long)K, a_fmt, (long long)need, (long long)RL_NOALLOC_SCRATCH_BYTES);
+  uint8_t* ws = nullptr;
+  if ((s = scratch_for_current_device(&ws))) return s;
+  return rl_bfp16_gemm_ws(A, a_fmt, lda, B_packed, C, ldc, M, N, K, ep, need > 0 ? ws : nullptr, need, stream);
 }
 
 int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, void* stream) {

@@ -21,6 +21,7 @@ RL_EP_QUANTIZE_OUT = 1
 RL_NORM_LAYER, RL_NORM_RMS = 0, 1
 RL_BRANCH_BF16, RL_BRANCH_PACKED = 0, 1
 RL_MAX_GROUP = 16
+RL_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _ERRNAMES = {1: "RL_ERR_NULL", 2: "RL_ERR_SHAPE", 3: "RL_ERR_ARG", 4: "RL_ERR_ALIGN", 5: "RL_ERR_DEVICE",
              6: "RL_ERR_WORKSPACE"}
@@ -56,6 +57,8 @@ SIGNATURES = {
                                         _P, _I64, _P]),
     "rl_bfp16_gemm_workspace_bytes": (ctypes.c_int64, [_I64, _I64, _I64]),
     "rl_bfp16_gemm_workspace_size": (ctypes.c_int64, [_I32, _I64, _I64, _I64]),
+    "rl_bfp16_gemm_noalloc": (ctypes.c_int, [_P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(Epilogue),
+                                             _P]),
     "rl_bfp16_gemm_grouped": (ctypes.c_int, [ctypes.POINTER(GemmDesc), _I32, _I32, _P]),
     "rl_bfp16_gemv": (ctypes.c_int, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I32, _P]),
     "rl_ln_modulate": (ctypes.c_int, [_P, _I64, _P, _I32, _I64, _P, _I64, _I32, _P, _I64, _P, _I32, _P, _I64, _I64,

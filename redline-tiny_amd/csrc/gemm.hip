@@ -19,6 +19,8 @@
 //   * workgroups are remapped so each XCD walks a contiguous range of tiles, grouped kGroupM M-tiles at a time.
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include <mutex>
 
@@ -218,11 +220,11 @@ __device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep
 // product already applied) of `nquads` row quads x W staged columns in the row-quad layout; staged column c is output
 // column c0 + c. Each thread takes blocks of 4 rows x 8 columns: gate / residual, bf16 rounding, optional
 // re-quantize, one 16-byte store per row.
-template <int W>
+template <int W, int NTH = kG8ThreadsDecl>
 __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, int r0, int c0, int nquads, int nout,
                                           int tid) {
   constexpr int kBlocks = W / 8;
-  for (int it = tid; it < nquads * kBlocks; it += kG8ThreadsDecl) {
+  for (int it = tid; it < nquads * kBlocks; it += NTH) {
     const int q = it / kBlocks, cb = it % kBlocks;
     const int col = c0 + 8 * cb;
     if (col >= nout) continue;
@@ -937,6 +939,246 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
   }
 }
 
+// ---- 4-wave kernel for bf16 A: one wave per SIMD, tiles of 64 MF rows x 128 columns ----------------------------
+// With one wave per SIMD a wave may hold 512 registers, so wave w owns rows 16 MF w .. +16 MF - 1 and all eight
+// 16-column groups of the tile: MF x 8 MFMA 16x16x32 accumulators. Against the 8-wave kernel (256 x 256 tiles,
+// waves of 128 x 64), per MFMA this halves the B decode (one 64 x 128 b_layout tile per K step serves 64 MF rows)
+// and cuts the operand reads from LDS by a third (8 A + 8 B fragments feed 64 MFMAs), the two costs that keep the
+// matrix pipe from issuing back to back. For SwiGLU the tile's groups 0..3 are the gate columns and 4..7 the proj
+// columns of the same 64 output columns, so silu(gate) * proj pairs share lane and register.
+//
+// LDS: two A stages (64 MF rows x 64 bf16, the 16-byte chunk swizzle, direct-to-LDS loads) and two B stages (the
+// step's 1024 decoded blocks as MFMA operands, fragment (group g, K half h) at 1 KB * (2 g + h), lane l's block at
+// 16 frag_pos(l)). Per K step k (A and B stage k % 2):
+//   phase 0: MFMAs on K half 0; read K half 1 of step k; decode raw B(k+1) (4 blocks per thread) into B stage
+//            (k+1) % 2, whose last reads were in phase 0 of step k-1; load raw B(k+2); wait for A(k+1); barrier.
+//   phase 1: MFMAs on K half 1; read K half 0 of step k+1; DMA A(k+2) into A stage k % 2 (last read in phase 0).
+// The loop body has no branches; loads past the last step re-read step KT-1 into stages never read again.
+constexpr int kW4Threads = 256;
+constexpr int kW4BStage = 1024 * 16;  // decoded blocks of one 64 x 128 b_layout tile
+constexpr int kW4GroupM = 2;           // M-tiles per group in an XCD's tile range (x 16 N-tiles: 32 CUs)
+
+template <int G, int MF>
+__global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G> args) {
+  constexpr int TM = 64 * MF;       // tile rows: 16 MF per wave, four waves down
+  constexpr int kAS = TM * BK * 2;  // bytes of one A stage
+  constexpr int kDma = TM / 32;     // A loads of 8 rows per wave per stage
+  static_assert(2 * kAS + 2 * kW4BStage <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kAS + 2 * kW4BStage];
+  uint8_t* const bl = lds + 2 * kAS;
+
+  const int pid = xcd_remap(blockIdx.x, gridDim.x);
+  int di = 0;
+  if constexpr (G > 1) {
+    for (int i = 1; i < args.n; i++)
+      if (pid >= args.d[i].tile_start) di = i;
+  }
+  const GemmDesc& d = args.d[di];
+  const int local = pid - d.tile_start;
+  const int group = local / (kW4GroupM * d.tiles_n);
+  const int first_m = group * kW4GroupM;
+  const int gm = min(d.tiles_m - first_m, kW4GroupM);
+  const int in_group = local - group * kW4GroupM * d.tiles_n;
+  const int m0 = (first_m + in_group % gm) * TM;
+  const int n0 = (in_group / gm) * 128;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS and row offsets stay scalar
+  const int KT = d.K / BK;
+  const bool swiglu = d.act == RL_ACT_SWIGLU;
+
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)d.B, (short)0, (int)((int64_t)d.K * d.N / 8 * 9), 0x00020000);
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)d.A, (short)0, (int)(((int64_t)d.M - 1) * d.lda * 2 + (int64_t)d.K * 2), 0x00020000);
+
+  // B decode: thread t decodes blocks 4t .. 4t + 3 of the step's b_layout tile, a 36-byte dword-aligned run, read
+  // with three loads (bytes 0..15, 16..31, 32..35). The four blocks are lanes 4 (t % 16) + J of fragment t / 16 =
+  // 2 g + h (column group g, K half h).
+  const uint32_t vb = (uint32_t)((int64_t)(n0 >> 7) * KT * kTileBytes + 36 * tid);
+  uint32_t st_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) st_off[j] = (tid >> 4) * 1024 + 16 * frag_pos(4 * (tid & 15) + j);
+  u32x4 raw0, raw1;  // bytes 0..15, 16..31 of the run
+  uint32_t raw2;     // bytes 32..35
+  auto load_raw = [&](int k, int part) {
+    if (part == 0) raw0 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, vb, k * kTileBytes, 0));
+    if (part == 1)
+      raw1 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, vb, k * kTileBytes + 16, 0));
+    if (part == 2) raw2 = __builtin_amdgcn_raw_buffer_load_b32(brs, vb, k * kTileBytes + 32, 0);
+  };
+  // block J (0..3) of the run: E at byte 9 J, q at bytes 9 J + 1 .. 9 J + 8 (compile-time byte positions)
+  auto decode_store = [&]<int J>(uint8_t* stage) {
+    const uint32_t dw[9] = {raw0.x, raw0.y, raw0.z, raw0.w, raw1.x, raw1.y, raw1.z, raw1.w, raw2};
+    constexpr int base = 0;
+    auto sbyte = [&](int b) { return (float)(int8_t)(dw[(b - base) >> 2] >> (8 * ((b - base) & 3))); };
+    constexpr int e = 9 * J;
+    const float sc = block_scale((dw[(e - base) >> 2] >> (8 * ((e - base) & 3))) & 0xFFu);
+    u32x4 o;
+    o.x = pack_hi(sbyte(e + 1) * sc, sbyte(e + 2) * sc);
+    o.y = pack_hi(sbyte(e + 3) * sc, sbyte(e + 4) * sc);
+    o.z = pack_hi(sbyte(e + 5) * sc, sbyte(e + 6) * sc);
+    o.w = pack_hi(sbyte(e + 7) * sc, sbyte(e + 8) * sc);
+    *reinterpret_cast<u32x4*>(stage + st_off[J]) = o;
+  };
+  // A: a stage is TM / 8 loads of 8 rows (64 lanes x 16 bytes); wave w issues loads g = kDma w + i. Load g covers
+  // row r = 8 g + lane / 8, 16-byte chunk (lane % 8) ^ swz(r); swz(r + 16) = swz(r), so loads i and i + 2 differ by
+  // 16 rows in the same chunk pattern: two base offsets plus a uniform row step, added in the vector offset (the
+  // buffer range check covers the vector offset), the K step in the scalar offset. Rows past M lie past the end of
+  // the buffer resource and read zeros.
+  const int ar0 = 8 * kDma * wave + (lane >> 3);
+  const uint32_t va_e = (uint32_t)(((int64_t)(m0 + ar0) * d.lda + ((lane & 7) ^ a_swz(ar0)) * 8) * 2);
+  const uint32_t va_o = (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + ((lane & 7) ^ a_swz(ar0 + 8)) * 8) * 2);
+  const uint32_t row16 = (uint32_t)(16 * d.lda * 2);
+  auto dma_a = [&](int stage, int k, int i) {
+    uint8_t* dst = lds + stage * kAS + 8 * (kDma * wave + i) * (BK * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16,
+                                             ((i & 1) ? va_o : va_e) + (uint32_t)(i >> 1) * row16, k * BK * 2, 0, 0);
+  };
+
+  f32x4 acc[MF][8];
+#pragma unroll
+  for (int mf = 0; mf < MF; mf++)
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[mf][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int arow = lane & 15;
+  const uint32_t aoff0 = 16 * MF * wave * (BK * 2) + arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
+  const uint32_t aoff1 = 16 * MF * wave * (BK * 2) + arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
+  const uint32_t boff = 16 * frag_pos(lane);
+  bf16x8 fa[MF], fb0[8], fb1[8];
+  auto read_a = [&](const uint8_t* p, int mf) { return *reinterpret_cast<const bf16x8*>(p + mf * 16 * (BK * 2)); };
+  auto read_b = [&](const uint8_t* p, int j) { return *reinterpret_cast<const bf16x8*>(p + j * 2048); };
+
+  // prologue: A(0) and B(0) in stage 0, A(1) in flight to stage 1, raw B(1) in registers (in flight), raw B(2)
+  // issued in phase 0 of step 0
+  const int k1 = min(1, KT - 1);
+#pragma unroll
+  for (int i = 0; i < kDma; i++) dma_a(0, 0, i);
+  load_raw(0, 0);
+  load_raw(0, 1);
+  load_raw(0, 2);
+  wait_vm<0>();
+  decode_store.template operator()<0>(bl);
+  decode_store.template operator()<1>(bl);
+  decode_store.template operator()<2>(bl);
+  decode_store.template operator()<3>(bl);
+  load_raw(k1, 0);
+  load_raw(k1, 1);
+  load_raw(k1, 2);
+#pragma unroll
+  for (int i = 0; i < kDma; i++) dma_a(1, k1, i);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; j++) fb0[j] = read_b(bl + boff, j);
+#pragma unroll
+  for (int mf = 0; mf < MF; mf++) fa[mf] = read_a(lds + aoff0, mf);
+
+  // One phase in octets (row fragment mf: its 8 MFMAs, then the next phase's fragment mf read into the same
+  // registers), scheduling fences between octets. The next phase's B fragments are read one per octet (the last
+  // octet reads what MF < 8 leaves), so LDS reads never come in bursts. P = 0 also decodes raw B(k+1) into stage ds
+  // (block J in octet J) and issues the three loads of raw B(kl) in octets 4..6 (MF = 6: 3..5); P = 1 issues the
+  // DMA of A(kl) into A stage sa, two loads per octet.
+  auto phase = [&]<int P>(bf16x8(&cur)[8], bf16x8(&nxt)[8], const uint8_t* na, const uint8_t* nb, uint8_t* ds, int kl,
+                          int sa) {
+    constexpr int kRaw0 = MF >= 7 ? 4 : 3;
+#pragma unroll
+    for (int mf = 0; mf < MF; mf++) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mf], cur[j], acc[mf][j], 0, 0, 0);
+        if (j == 1) nxt[mf] = read_b(nb, mf);
+        if (mf == MF - 1 && j >= 2 && MF + j - 2 < 8) nxt[MF + j - 2] = read_b(nb, MF + j - 2);
+      }
+      fa[mf] = read_a(na, mf);
+      if constexpr (P == 0) {
+        if (mf == 0) decode_store.template operator()<0>(ds);
+        if (mf == 1) decode_store.template operator()<1>(ds);
+        if (mf == 2) decode_store.template operator()<2>(ds);
+        if (mf == 3) decode_store.template operator()<3>(ds);
+        if (mf >= kRaw0 && mf < kRaw0 + 3) load_raw(kl, mf - kRaw0);
+        constexpr int kMfma = 0x008, kValu = 0x002, kDsWrite = 0x200;
+        if (mf < 4) {
+#pragma unroll
+          for (int g = 0; g < 8; g++) {
+            __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kValu, 3, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(kValu, 8, 0);
+          __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
+        }
+      } else {
+        if (2 * mf < kDma) dma_a(sa, kl, 2 * mf);
+        if (2 * mf + 1 < kDma) dma_a(sa, kl, 2 * mf + 1);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  for (int k = 0; k < KT; k++) {
+    const int s0 = k & 1, s1 = s0 ^ 1;
+    const int kl = min(k + 2, KT - 1);
+    // phase 0: MFMAs on half 0 of step k, read half 1 of step k, decode B(k+1) into stage s1, load raw B(k+2)
+    phase.template operator()<0>(fb0, fb1, lds + s0 * kAS + aoff1, bl + s0 * kW4BStage + 1024 + boff,
+                                 bl + s1 * kW4BStage, kl, s0);
+    wait_vm<3>();  // A(k+1) done; the three raw B(k+2) loads may stay in flight
+    __syncthreads();
+    // phase 1: MFMAs on half 1, read half 0 of step k+1, DMA A(k+2) into stage s0
+    phase.template operator()<1>(fb1, fb0, lds + s1 * kAS + aoff0, bl + s1 * kW4BStage + boff, nullptr, kl, s0);
+  }
+  wait_vm<0>();
+  __syncthreads();
+
+  // ---- epilogue: bias and activation (SwiGLU: silu(gate) * proj of groups g and g + 4) in registers, fp32 results
+  // staged in LDS in the row-quad layout, then finished 8 columns at a time by all threads (ep8_finish)
+  float* ep = reinterpret_cast<float*>(lds);
+  const int col_in = lane & 15;
+  const int nout = swiglu ? d.N / 2 : d.N;
+  float bj[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) bj[j] = d.bias ? d.bias[n0 + 16 * j + col_in] : 0.f;
+  if (swiglu) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int c = ep_slot(16 * g + col_in);
+#pragma unroll
+      for (int mf = 0; mf < MF; mf++) {
+        f32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = silu_f(acc[mf][g][i] + bj[g]) * (acc[mf][g + 4][i] + bj[g + 4]);
+        *reinterpret_cast<f32x4*>(ep + ((4 * MF * wave + 4 * mf + (lane >> 4)) * 64 + c) * 4) = v;
+      }
+    }
+    __syncthreads();
+    ep8_finish<64, kW4Threads>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
+  } else {
+    const bool gelu = d.act == RL_ACT_GELU_TANH;
+#pragma unroll
+    for (int P = 0; P < 2; P++) {
+      if ((wave >> 1) == P) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int c = ep_slot(16 * j + col_in);
+#pragma unroll
+          for (int mf = 0; mf < MF; mf++) {
+            f32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              v[i] = acc[mf][j][i] + bj[j];
+              if (gelu) v[i] = gelu_tanh_f(v[i]);
+            }
+            *reinterpret_cast<f32x4*>(ep + ((4 * MF * (wave & 1) + 4 * mf + (lane >> 4)) * 128 + c) * 4) = v;
+          }
+        }
+      }
+      __syncthreads();
+      ep8_finish<128, kW4Threads>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
+      __syncthreads();
+    }
+  }
+}
+
 template <int G>
 static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, uint16_t* C, int64_t ldc, int64_t M,
                      int64_t N, int64_t K, const rl_epilogue* ep, int32_t a_fmt, int tile_start) {
@@ -1007,6 +1249,72 @@ static Plan8 plan8(int64_t M, int64_t N, int cus) {
   return best;
 }
 
+// ---- whole-K plan over both kernels -----------------------------------------------------------------------------
+// A tile of the 4-wave kernel (64 mf rows x 128 columns) costs about mf + kTileFixed4 in the 8-wave kernel's units
+// (a 256 x 256 tile of MF = 8 costs 9.5): per round of the CUs it runs ~6% faster than the 8-wave kernel on the same
+// FLOPs, because it decodes half the B blocks per MFMA and reads a third fewer operand bytes from LDS (measured on
+// the DiT FFN shapes, bit-identical results). Its last M-tile may be partial. The plan is one launch, or a first
+// launch over rows [0, split) and a second one of the 8-wave kernel over the rest.
+constexpr double kTileFixed4 = 0.9;
+constexpr int kMf4Choices[] = {8, 7, 6};
+
+static int64_t tiles4(int64_t M, int64_t N, int mf) { return ((M + 64 * mf - 1) / (64 * mf)) * (N / 128); }
+static double launch_cost4(int64_t tiles, int mf, int cus) {
+  return (double)((tiles + cus - 1) / cus) * (mf + kTileFixed4);
+}
+
+struct PlanG {
+  bool w4;        // the first launch runs the 4-wave kernel
+  int mf;         // its fragment count
+  int64_t split;  // rows of the first launch; 0 = one launch over all rows
+  int mf_tail;    // fragments per wave of the 8-wave second launch
+};
+
+// RLBFP_GEMM_KERNEL=4w or 8w restricts the plan to plans whose first launch runs that kernel (for A/B measurements).
+static int kernel_restriction() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("RLBFP_GEMM_KERNEL");
+    v = e && strcmp(e, "4w") == 0 ? 1 : (e && strcmp(e, "8w") == 0 ? 2 : 0);
+  }
+  return v;
+}
+
+static PlanG plan_gemm(int64_t M, int64_t N, int cus, int act) {
+  // the tanh GELU epilogue's transcendentals cost more on one wave per SIMD than they save in the main loop
+  // (measured at 4096 x 3072 x 3072: 102 against 97 us), so GELU stays on the 8-wave kernel unless forced
+  const int only = kernel_restriction() ? kernel_restriction() : (act == RL_ACT_GELU_TANH ? 2 : 0);
+  PlanG best{false, 8, 0, 8};
+  double bc = 1e300;
+  auto best_tail = [&](int64_t rows, int& mf_out) {
+    double c = 1e300;
+    for (int mf : kMfChoices) {
+      const double t = launch_cost(tiles8(rows, N, mf), mf, cus);
+      if (t < c) { c = t; mf_out = mf; }
+    }
+    return c;
+  };
+  if (only != 1) {
+    const Plan8 p = plan8(M, N, cus);
+    double c = launch_cost(tiles8(p.split ? p.split : M, N, p.mf), p.mf, cus);
+    if (p.split) c += kSecondLaunch + launch_cost(tiles8(M - p.split, N, p.mf_tail), p.mf_tail, cus);
+    bc = c;
+    best = PlanG{false, p.mf, p.split, p.mf_tail};
+  }
+  if (only != 2) {
+    for (int mf : kMf4Choices) {
+      const double c = launch_cost4(tiles4(M, N, mf), mf, cus);
+      if (c < bc) { bc = c; best = PlanG{true, mf, 0, 8}; }
+      for (int64_t R = 64 * mf; R < M; R += 64 * mf) {
+        int mt = 8;
+        const double c2 = launch_cost4(tiles4(R, N, mf), mf, cus) + kSecondLaunch + best_tail(M - R, mt);
+        if (c2 < bc) { bc = c2; best = PlanG{true, mf, R, mt}; }
+      }
+    }
+  }
+  return best;
+}
+
 // ---- K split (one GEMM whose tiles fill few CUs: small M, deep K) ------------------------------------------------
 // Model, in microseconds at the running clock: a tile of MF fragments costs kStepUs (MF + 1) per K step plus kTileUs
 // (prologue and epilogue), and a launch of T tiles takes ceil(T / CUs) such rounds. The reduce launch reads the
@@ -1052,6 +1360,7 @@ static void set_tiles8(GemmArgs<G>& args, int mf, int& total) {
   for (int i = 0; i < args.n; i++) {
     GemmDesc& g = args.d[i];
     g.tiles_m = (int32_t)((g.M + 32 * mf - 1) / (32 * mf));
+    g.tiles_n = (int32_t)((g.N + BN - 1) / BN);
     g.tile_start = total;
     total += g.tiles_m * g.tiles_n * g.ksplit;
   }
@@ -1067,6 +1376,32 @@ static int launch8(const GemmArgs<G>& args, int total_tiles, int mf, void* strea
     case 7: hipLaunchKernelGGL((gemm8_kernel<G, 7>), grid, block, 0, st, args); break;
     case 6: hipLaunchKernelGGL((gemm8_kernel<G, 6>), grid, block, 0, st, args); break;
     default: hipLaunchKernelGGL((gemm8_kernel<G, 4>), grid, block, 0, st, args); break;
+  }
+  return launch_status("rl_bfp16_gemm");
+}
+
+// Tiles of the 4-wave kernel: 64 mf rows x 128 columns (one b_layout N-tile); whole K only.
+template <int G>
+static void set_tiles4w(GemmArgs<G>& args, int mf, int& total) {
+  total = 0;
+  for (int i = 0; i < args.n; i++) {
+    GemmDesc& g = args.d[i];
+    g.tiles_m = (int32_t)((g.M + 64 * mf - 1) / (64 * mf));
+    g.tiles_n = (int32_t)(g.N / 128);
+    g.tile_start = total;
+    total += g.tiles_m * g.tiles_n;
+  }
+  for (int i = args.n; i < G; i++) args.d[i] = args.d[args.n - 1];
+}
+
+template <int G>
+static int launch4w(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(total_tiles), block(kW4Threads);
+  switch (mf) {
+    case 8: hipLaunchKernelGGL((gemm4w_kernel<G, 8>), grid, block, 0, st, args); break;
+    case 7: hipLaunchKernelGGL((gemm4w_kernel<G, 7>), grid, block, 0, st, args); break;
+    default: hipLaunchKernelGGL((gemm4w_kernel<G, 6>), grid, block, 0, st, args); break;
   }
   return launch_status("rl_bfp16_gemm");
 }
@@ -1169,17 +1504,21 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
       return launch_status("rl_bfp16_gemm (reduce)");
     }
   }
-  const Plan8 p = plan8(M, N, device_cus());
-  if (p.split == 0) {
-    set_tiles8(args, p.mf, total);
-    return launch8<1>(args, total, p.mf, stream);
-  }
+  const PlanG p = plan_gemm(M, N, device_cus(), ep ? ep->act : RL_ACT_NONE);
   GemmArgs<1> tail;
-  tail.d[0] = rows_from(args.d[0], p.split);
-  tail.n = 1;
-  args.d[0].M = (int32_t)p.split;
-  set_tiles8(args, p.mf, total);
-  if ((s = launch8<1>(args, total, p.mf, stream))) return s;
+  if (p.split) {
+    tail.d[0] = rows_from(args.d[0], p.split);
+    tail.n = 1;
+    args.d[0].M = (int32_t)p.split;
+  }
+  if (p.w4) {
+    set_tiles4w(args, p.mf, total);
+    s = launch4w<1>(args, total, p.mf, stream);
+  } else {
+    set_tiles8(args, p.mf, total);
+    s = launch8<1>(args, total, p.mf, stream);
+  }
+  if (s || !p.split) return s;
   set_tiles8(tail, p.mf_tail, total);
   return launch8<1>(tail, total, p.mf_tail, stream);
 }

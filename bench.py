@@ -8,9 +8,9 @@ bf16 activations ~N(0, 1), seed 0:
 The metric is the step's GEMM throughput (2MNK summed over both GEMMs, quantize time included) in TFLOP/s, the step
 captured once as a HIP graph and replayed (its eager time, launched from Python, is reported beside it). The
 roofline object is for the dominant kernel, the up GEMM (657.13 GFLOP per call), against the dense bf16 MFMA peak; the
-library runs that call as two launches of the same kernel (rows 0..4095 in 256-row tiles, six full rounds of the 256
-CUs, then the last 256 rows in 128-row tiles), timed together. Kernel times are medians of HIP-event intervals on the
-launch stream.
+library runs that call as two launches (the 4-wave kernel over rows 0..4095 in 512 x 128 tiles, six full rounds of the
+256 CUs, then the 8-wave kernel over the last 256 rows in 128 x 256 tiles), timed together. Kernel times are medians of
+HIP-event intervals on the launch stream.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
 rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
 produces the up GEMM's A (4352 x 3072) and the QKV post pass (4352 tokens x 24 heads) in GB/s against HBM; attention
@@ -156,6 +156,8 @@ def gpu_bench(steps, warmup, no_configs=False):
     torch.cuda.synchronize()
     ms_step = g0.elapsed_time(g1) / steps
     assert torch.equal(y, y_eager), "graph replay of the step differs from the eager result"
+    h_step = h.clone()
+    v9a = v9a_bench(inp, xq, h_step)
 
     # the quantize pass alone: a ~12 us kernel whose event interval inside the eager step also holds a kernel
     # boundary, so it is timed like the GEMV, in graph replays rotating over 4 inputs and outputs (274 MB > MALL)
@@ -213,11 +215,32 @@ def gpu_bench(steps, warmup, no_configs=False):
         "wall_s": wall, "ms_step": ms_step, "ms_step_eager": ms_step_eager,
         "ms_q": ms_q, "us_q_alone": us_q_alone, "ms_up": ms_up, "ms_down": ms_down, "us_gemv": us_gemv,
         "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
+        "v9a": v9a,
         "ln": ln_bench(dev),
         "qkv": qkv_bench(dev),
         "attn": attn_bench(dev),
         "configs": None if no_configs else configs_bench(dev),
     }
+
+
+def v9a_bench(inp, xq, h_step, per_graph=10, reps=3):
+    """The up GEMM with A as the reference passes it, the a_layout bfp16 stream (V9), beside the same GEMM on the bf16
+    A of the quantize pass, both as HIP-graph replays: the library decodes the stream into a bf16 copy in the
+    workspace (one HBM-bound launch), then runs the bf16-A kernels. Both must give the step's H bit for bit."""
+    import torch
+
+    from rlbfp import ops
+
+    xa, _ = ops.quantize(inp["x"], order="a_layout")
+    h = torch.empty_like(h_step)
+    out = {}
+    for name, a, kw in (("bf16", xq, {}), ("v9a_staged", xa, {"M": M, "a_fmt": "packed_a_layout"})):
+        def call(i):
+            ops.gemm(a, inp["up"], 2 * FF, K, act="swiglu", quantize_out=True, out=h, **kw)
+        us = graph_us(call, 3, per_graph, reps)
+        assert torch.equal(h, h_step), f"up GEMM with {name} A differs from the step's"
+        out[name + "_us"] = round(us, 2)
+    return out
 
 
 def ln_bench(dev, sets=4, per_graph=40, reps=4):
@@ -544,7 +567,7 @@ def sustain(seconds):
     a_q = ops.quantize(a, deq=True)[1]
     h = torch.empty((M, FF), dtype=torch.bfloat16, device=dev)
     w_bf = w_up.to(torch.bfloat16)
-    runs = {"gemm8 up GEMM + SwiGLU (bfp16 weights)":
+    runs = {"up GEMM + SwiGLU (bfp16 weights)":
             lambda: ops.gemm(a_q, packed, 2 * FF, K, act="swiglu", quantize_out=True, out=h),
             "torch bf16 linear, same shape": lambda: torch.nn.functional.linear(a_q, w_bf)}
     for name, fn in runs.items():
@@ -623,7 +646,7 @@ def main():
                    "weights": "bfp16ebs8 ~N(0,0.02)", "activations": "bf16 ~N(0,1)", "seed": 0},
         "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(up_tflops / PEAK_BF16_TFLOPS, 4), "traffic": UP_GEMM_TRAFFIC_BYTES,
-                     "kernel": "gemm8_kernel up GEMM 4352x3072x24576 + SwiGLU (256-row + 128-row launches)",
+                     "kernel": "up GEMM 4352x3072x24576 + SwiGLU: gemm4w_kernel<1,8> rows 0..4095 + gemm8_kernel<1,4> rows 4096..4351",
                      "us": round(r["ms_up"] * 1e3, 2)},
         "kernels": {
             # the kernel alone (graph replays); algorithmic bytes: bf16 read + packed written (the pass also writes
@@ -634,6 +657,10 @@ def main():
             "up_us": round(r["ms_up"] * 1e3, 2), "up_tflops": round(up_tflops, 2),
             "down_us": round(r["ms_down"] * 1e3, 2),
             "down_tflops": round(flops_down() / (r["ms_down"] * 1e-3) / 1e12, 2),
+            # the up GEMM in graph replays, fed bf16 A, then the reference's a_layout A stream (same H bits)
+            "up_graph_us": r["v9a"]["bf16_us"],
+            "up_v9a_staged_us": r["v9a"]["v9a_staged_us"],
+            "up_v9a_vs_bf16": round(r["v9a"]["v9a_staged_us"] / r["v9a"]["bf16_us"], 4),
         },
         "gemv": {"shape": [1, GEMV_K, GEMV_N], "us": round(r["us_gemv"], 2), "gbps": round(r["gemv_gbps"], 1),
                  "frac_hbm": round(r["gemv_gbps"] / PEAK_HBM_GBPS, 4), "bytes": int(r["gemv_bytes"]),

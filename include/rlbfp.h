@@ -94,6 +94,9 @@ typedef struct rl_epilogue {
 } rl_epilogue;
 
 /* One GEMM. lda / ldc in elements (bf16); ldc >= Nout (N, or N/2 for SwiGLU). ep may be NULL (plain bf16 C).
+ * An A format other than RL_A_BF16 is staged as bf16 first (see rl_bfp16_gemm_ws) in a stream-ordered allocation
+ * (hipMallocAsync / hipFreeAsync on `stream`); on a stream under graph capture that is refused with
+ * RL_ERR_WORKSPACE, and rl_bfp16_gemm_ws with a workspace or rl_bfp16_gemm_noalloc serves instead.
  * Replaces forward.gemm / NPU.run(op, GEMMS[op, M], [A, B, C]) (redline/forward.py:194-197, :138-165), the ATB
  * microkernels matmul_vectorized_bfp16 (kernels/atb3/mm_bfp_mixed.cc:61, mm_bfp_rho.cc:64, vlm/mm_bfp_c16.cc:62)
  * and, with RL_ACT_SWIGLU, matmul_swiglu_bfp16 (kernels/atb3/mm_bfp_swiglu.cc:88). */
@@ -110,7 +113,7 @@ int rl_bfp16_gemm(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_pa
  *     values, one HBM-bound pass: 9/8 + 2 bytes per value), and the product then runs on the RL_A_BF16 kernel with
  *     the rest of the workspace. The result is the RL_A_BF16 path's on the staged values: bit-identical to
  *     rl_bfp16_gemm's for the same format unless the K split applies.
- * workspace NULL: exactly rl_bfp16_gemm (a non-bf16 A then takes the register-staged kernel, which is slower).
+ * workspace NULL: exactly rl_bfp16_gemm (a non-bf16 A then stages into a stream-ordered allocation).
  * workspace_bytes below what rl_bfp16_gemm_workspace_size() gives for the shape and format: RL_ERR_WORKSPACE for a
  * non-bf16 A that the staged copy does not fit; otherwise the planner runs whole K. Calls that share a workspace on
  * different streams race. Same reference interface as rl_bfp16_gemm (redline/forward.py:194-197). */
@@ -137,7 +140,8 @@ int rl_bfp16_gemm_noalloc(const void *A, int32_t a_fmt, int64_t lda, const uint8
                           int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *stream);
 
 /* Several independent GEMMs (different shapes, weights and epilogues, one A format) in one launch, e.g. the image-
- * and text-stream projections of a DiT block. At most RL_MAX_GROUP descriptors. Replaces the per-op sequence of
+ * and text-stream projections of a DiT block. At most RL_MAX_GROUP descriptors. A non-bf16 A format stages every
+ * member's A as bf16 first, in one stream-ordered allocation (as rl_bfp16_gemm does). Replaces the per-op sequence of
  * CachedStep.blocks (redline/forward.py:240-254) for GEMMs that do not depend on each other. */
 #define RL_MAX_GROUP 16
 typedef struct rl_gemm_desc {

@@ -1,22 +1,20 @@
 // bfp16-weight GEMM for gfx950: C = epilogue(A @ B), B streamed from HBM in the packed b_layout(64, 128) order that
-// redline/pack_weights.py:72-79 writes, decoded to bf16 in registers, bf16 MFMA with fp32 accumulation.
+// redline/pack_weights.py:72-79 writes, decoded to bf16 on chip, bf16 MFMA (16x16x32) with fp32 accumulation.
 //
 // Replaces the ATB microkernels (kernels/atb3/mm_bfp_mixed.cc:61, mm_bfp_rho.cc:64, kernels/vlm/mm_bfp_c16.cc:62)
 // and the SwiGLU-flush GEMM (kernels/atb3/mm_bfp_swiglu.cc:88) behind forward.gemm / NPU.run (redline/forward.py).
 //
-// Tiling (one 256x256 output tile per workgroup, 4 waves, K steps of 64):
-//   * wave w owns four 16-column groups of the tile and all 256 rows: 16 x 4 MFMA 16x16x32 accumulators (256 fp32
-//     per lane). Its groups are 4w..4w+3, or for SwiGLU the gate groups {g, g+1} and proj groups {g+4, g+5} of one
-//     128-column tile, so silu(gate) * proj pairs sit in the same lane and register.
-//   * B never touches LDS: in the b_layout a 16-column group x 32 K is 64 consecutive 9-byte blocks (576 bytes),
-//     and lane l's MFMA operand (column l%16, K 8(l/16)..+7) is exactly block l. Each lane reads its block through a
-//     dword-aligned 12-byte window and decodes it (sign-extending byte converts, one scale multiply, bf16 packing).
-//     Every B element is decoded once per workgroup.
-//   * A (bf16, row major) is staged through a double-buffered LDS tile (256 x 64 bf16 = 32 KB per stage) with a
-//     16-byte-chunk XOR swizzle; all four waves read it as ds_read_b128 operands.
-//   * loads run two K steps ahead: while the MFMAs of step k run, the raw B windows and the A chunks of step k+1
-//     are in flight; after them B(k+1) is decoded and A(k+1) stored to the other LDS stage.
-//   * workgroups are remapped so each XCD walks a contiguous range of tiles, grouped kGroupM M-tiles at a time.
+// Two whole-K kernels, both for bf16 A (bfp16 values), one workgroup per CU (160 KB of LDS), K steps of 64:
+//   * gemm8_kernel: 8 waves (two per SIMD), tiles of 32 MF rows x 256 columns. Each K step the waves decode the
+//     tile's raw B blocks once into an LDS stage of MFMA operands; A arrives by direct-to-LDS buffer loads.
+//   * gemm4w_kernel: 4 waves (one per SIMD), tiles of 64 MF rows x 128 columns, each wave 16 MF rows x all 128
+//     columns, so per MFMA it decodes half the B blocks and reads a third fewer operand bytes from LDS.
+// A planner picks the kernel and fragment count per shape from a rounds-of-the-CUs cost model, and may run the
+// rows past the last full round as a second launch of shorter tiles. Small-M, deep-K shapes may split K across
+// workgroups (fp32 partials in a workspace, summed by gemm_reduce_kernel). A non-bf16 A (the NPU's packed
+// a_layout stream, packed row blocks, or bf16 to be quantized) is first staged as bf16 in one HBM-bound pass.
+// The epilogue (bias, GELU or SwiGLU, gate * v + residual, bf16 rounding, re-quantize) runs from an LDS tile of
+// the fp32 accumulators.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -31,7 +29,6 @@
 namespace rl {
 
 constexpr int BM = 256, BN = 256, BK = 64;
-constexpr int kGThreads = 256;
 constexpr int kAStage = BM * BK * 2;  // bytes of one A stage
 constexpr int kTileBytes = 64 * 128 * 9 / 8;  // one b_layout tile (64 K x 128 N)
 // Tiles are walked kGroupM M-tiles at a time within each XCD's contiguous range: the 32 CUs of an XCD then hold a
@@ -61,26 +58,6 @@ struct GemmArgs {
   GemmDesc d[G];
   int32_t n;
 };
-
-// Scheduling pattern for one K step of the pipelined loop (two halves of 64 MFMAs, 16 A reads and ~104 decode
-// VALU ops each): four A reads up front, then per row fragment its 4 MFMAs with one A read (four fragments ahead)
-// and seven VALU ops between them, so that neither LDS latency nor the decode stalls the matrix pipe.
-__device__ __forceinline__ void interleave_schedule() {
-  constexpr int kMfma = 0x008, kValu = 0x002, kDsRead = 0x100;
-  __builtin_amdgcn_sched_group_barrier(kDsRead, 4, 0);
-#pragma unroll
-  for (int g = 0; g < 32; g++) {
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kValu, 1, 0);
-  }
-}
 
 // 16-byte chunk swizzle of the A tile: chunk c of row r is stored at chunk c ^ swz(r). A wave's ds_read_b128 of one
 // chunk column over 16 consecutive rows then spreads over all banks.
@@ -149,71 +126,6 @@ __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int oc
              pack_bf16_rne(v[6], v[7])};
   if (d.flags & RL_EP_QUANTIZE_OUT) o = requantize8(o);
   return o;
-}
-
-// Phase B of the epilogue for 64 rows starting at r0: the LDS tile holds the fp32 accumulators of computed columns
-// n0..n0+255 in the row-quad layout. Each thread takes 4 rows x 8 output columns (4 output blocks).
-template <int NT>
-__device__ __forceinline__ void epilogue_rows(const GemmDesc& d, const float* ep, int r0, int n0, int nout, int tid) {
-  auto quad = [&](int q, int c) { return *reinterpret_cast<const f32x4*>(ep + (q * 256 + ep_slot(c)) * 4); };
-  if (d.act == RL_ACT_SWIGLU) {
-    // 16 row quads x 16 gate blocks of 8 columns: one per thread; gate columns gc..gc+7, proj gc+64..gc+71
-    if (tid >= 256) return;
-    const int q = tid >> 4, ob = tid & 15;
-    const int gc = (ob >> 3) * 128 + (ob & 7) * 8;
-    if (n0 + gc >= d.N) return;
-    f32x4 g[8], p[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      g[k] = quad(q, gc + k);
-      p[k] = quad(q, gc + 64 + k);
-    }
-    float bg[8], bp[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      bg[k] = d.bias ? d.bias[n0 + gc + k] : 0.f;
-      bp[k] = d.bias ? d.bias[n0 + gc + 64 + k] : 0.f;
-    }
-    const int ocol = (((n0 + gc) >> 7) << 6) + ((n0 + gc) & 63);  // 64t + u, t = col / 128, u = col % 64
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = r0 + 4 * q + i;
-      if (row >= d.M) break;
-      float v[8];
-#pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = silu_f(g[k][i] + bg[k]) * (p[k][i] + bp[k]);
-      const u32x4 o = finish_block(d, row, ocol, nout, v);
-      *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
-    }
-  } else {
-    // 16 row quads x 32 column blocks
-#pragma unroll
-    for (int it = 0; it < 512 / NT; it++) {
-      const int b = it * NT + tid;
-      const int q = b >> 5, cb = b & 31;
-      const int col = n0 + cb * 8;
-      if (col >= d.N) continue;
-      f32x4 a[8];
-#pragma unroll
-      for (int k = 0; k < 8; k++) a[k] = quad(q, cb * 8 + k);
-      float bv[8];
-#pragma unroll
-      for (int k = 0; k < 8; k++) bv[k] = d.bias ? d.bias[col + k] : 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int row = r0 + 4 * q + i;
-        if (row >= d.M) break;
-        float v[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-          v[k] = a[k][i] + bv[k];
-          if (d.act == RL_ACT_GELU_TANH) v[k] = gelu_tanh_f(v[k]);
-        }
-        const u32x4 o = finish_block(d, row, col, nout, v);
-        *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
-      }
-    }
-  }
 }
 
 // Second half of the 8-wave kernel's epilogue. The LDS tile holds fp32 values (bias, activation and the SwiGLU
@@ -303,287 +215,6 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmDesc d) {
   }
   const u32x4 o = finish_block(d, row, ocol, nout, v);
   *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
-}
-
-// Loads this thread's eight 16-byte A chunks of K step kt: rows (tid>>3) + 32i, chunk tid&7.
-template <int AFMT>
-__device__ __forceinline__ void load_a(const GemmDesc& d, int m0, int kt, int tid, u32x4 (&av)[8]) {
-  const int c = tid & 7;
-  const int KB = d.K >> 3;  // K blocks per row
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int r = min(m0 + (tid >> 3) + 32 * i, d.M - 1);
-    if constexpr (AFMT == RL_A_BF16 || AFMT == RL_A_BF16_QUANTIZE) {
-      const uint16_t* p = static_cast<const uint16_t*>(d.A) + (int64_t)r * d.lda + kt * BK + c * 8;
-      av[i] = *reinterpret_cast<const u32x4*>(p);
-    } else {
-      int64_t blk;
-      const int kb = kt * 8 + c;
-      if constexpr (AFMT == RL_A_PACKED_ROWBLOCK) {
-        blk = (int64_t)r * KB + kb;
-      } else {  // A_LAYOUT: ((((mt*KT + kt)*8 + sbr)*8 + bc)*2 + bis)*8 + rib
-        const int KT = d.K >> 6;
-        blk = ((((((int64_t)(r >> 7) * KT + kt) * 8 + ((r >> 4) & 7)) * 8 + c) * 2 + ((r >> 3) & 1)) * 8) + (r & 7);
-      }
-      const Window w = load_window(static_cast<const uint8_t*>(d.A), blk * 9);
-      av[i] = u32x4{w.w0, w.w1, w.w2, (uint32_t)(blk & 3)};
-    }
-  }
-}
-
-// Converts the loaded A chunks to bf16 MFMA operands and stores them into an LDS stage.
-template <int AFMT>
-__device__ __forceinline__ void store_a(uint8_t* stage, int tid, const u32x4 (&av)[8]) {
-  const int c = tid & 7;
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int r = (tid >> 3) + 32 * i;
-    u32x4 v = av[i];
-    if constexpr (AFMT == RL_A_BF16_QUANTIZE) {
-      v = quantize_bf16x8(v);
-    } else if constexpr (AFMT == RL_A_PACKED_ROWBLOCK || AFMT == RL_A_PACKED_A_LAYOUT) {
-      v = __builtin_bit_cast(u32x4, decode_window(v.x, v.y, v.z, v.w));
-    }
-    *reinterpret_cast<u32x4*>(stage + r * (BK * 2) + ((c ^ a_swz(r)) << 4)) = v;
-  }
-}
-
-template <int AFMT, int G>
-__global__ __launch_bounds__(kGThreads, 1) void gemm_kernel(const GemmArgs<G> args) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[3 * kAStage];
-
-  const int pid = xcd_remap(blockIdx.x, gridDim.x);
-  int di = 0;
-  if constexpr (G > 1) {
-    for (int i = 1; i < args.n; i++)
-      if (pid >= args.d[i].tile_start) di = i;
-  }
-  const GemmDesc& d = args.d[di];
-  int local = pid - d.tile_start;
-  // K pieces: piece p covers K steps [p KT / ksplit, (p + 1) KT / ksplit) of every tile; tiles of one piece are
-  // consecutive in launch order
-  int piece = 0;
-  if (d.ksplit > 1) {
-    piece = local / (d.tiles_m * d.tiles_n);
-    local -= piece * d.tiles_m * d.tiles_n;
-  }
-  const int group = local / (kGroupM * d.tiles_n);
-  const int first_m = group * kGroupM;
-  const int gm = min(d.tiles_m - first_m, kGroupM);
-  const int in_group = local - group * kGroupM * d.tiles_n;
-  const int m0 = (first_m + in_group % gm) * BM;
-  const int n0 = (in_group / gm) * BN;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int KT = d.K / BK;
-  const int N = d.N;
-
-  // this wave's four 16-column groups
-  int grp[4];
-  if (d.act == RL_ACT_SWIGLU) {
-    const int g = 8 * (wave >> 1) + 2 * (wave & 1);
-    grp[0] = g; grp[1] = g + 1; grp[2] = g + 4; grp[3] = g + 5;
-  } else {
-#pragma unroll
-    for (int j = 0; j < 4; j++) grp[j] = 4 * wave + j;
-  }
-  const bool active = n0 + 16 * grp[0] < d.N;  // a wave's groups share one 128-column tile; N % 128 == 0
-
-  // byte offsets of this lane's B windows at K step 0, K half 0; step kt adds kt * 9216, half h adds 576
-  const uint8_t* bptr[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int col = n0 + 16 * grp[j];
-    const int64_t t = active ? (int64_t)(col >> 7) * KT : 0;
-    const int sbc = (col >> 4) & 7;
-    bptr[j] = d.B + ((t * kTileBytes + (int64_t)(sbc * 128 + lane) * 9) & ~(int64_t)3);
-  }
-  const uint32_t bo = lane & 3;  // byte offset of the block inside its window: (9 * lane) % 4
-
-  f32x4 acc[16][4];
-#pragma unroll
-  for (int mf = 0; mf < 16; mf++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[mf][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // A operand read addresses: row 16mf + lane%16, chunk 4h + lane/16 (swizzled); the swizzle depends only on lane
-  const int arow = lane & 15;
-  const int aoff0 = arow * (BK * 2) + (((lane >> 4) ^ a_swz(arow)) << 4);
-  const int aoff1 = arow * (BK * 2) + (((4 + (lane >> 4)) ^ a_swz(arow)) << 4);
-
-  bf16x8 bcur[4][2];
-  // MFMAs of one K half (h) of one step over the 16 row fragments, with the A stage at st
-  // (A fragments are read four row fragments ahead of their MFMAs, so that LDS latency hides under MFMAs)
-  auto mfma_half = [&](const uint8_t* st, int aoff, int h) {
-    constexpr int kAhead = 4;
-    bf16x8 a[kAhead];
-#pragma unroll
-    for (int mf = 0; mf < kAhead; mf++) a[mf] = *reinterpret_cast<const bf16x8*>(st + mf * 16 * (BK * 2) + aoff);
-#pragma unroll
-    for (int mf = 0; mf < 16; mf++) {
-      const bf16x8 cur = a[mf % kAhead];
-      if (mf + kAhead < 16)
-        a[mf % kAhead] = *reinterpret_cast<const bf16x8*>(st + (mf + kAhead) * 16 * (BK * 2) + aoff);
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur, bcur[j][h], acc[mf][j], 0, 0, 0);
-    }
-  };
-
-  if constexpr (AFMT == RL_A_BF16) {
-    // ---- pipelined path: A by direct-to-LDS loads into 3 stages, B windows in 3 register slots, both issued two
-    // steps ahead. Within a step, the B half not being multiplied is decoded under the MFMAs of the other half:
-    // first half (K 0..31 of the step) decodes this step's second half, second half decodes the next step's first.
-    // Buffer loads: the per-lane byte offsets are fixed for the whole K loop and the K step enters as a scalar
-    // offset, so no per-step address registers are needed. Out-of-range offsets read zero.
-    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-    const __amdgpu_buffer_rsrc_t brs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)d.B, (short)0, (int)((int64_t)d.K * d.N / 8 * 9), 0x00020000);
-    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)d.A, (short)0, (int)(((int64_t)d.M - 1) * d.lda * 2 + (int64_t)d.K * 2), 0x00020000);
-    uint32_t vb[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) vb[j] = (uint32_t)(bptr[j] - d.B);
-    u32x3 raw[3][4][2];
-    auto load_raw = [&](u32x3 (&r)[4][2], int kt) {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) r[j][h] = __builtin_amdgcn_raw_buffer_load_b96(brs, vb[j] + h * 576, kt * kTileBytes, 0);
-    };
-    auto decode_half = [&](const u32x3 (&r)[4][2], int h) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) bcur[j][h] = decode_window(r[j][h].x, r[j][h].y, r[j][h].z, bo);
-    };
-    // wave w fills rows 64w..64w+63 of a stage: 8 loads of 8 rows; lane l -> row +l/8, LDS chunk l%8, which holds
-    // logical chunk (l%8) ^ swz(row)
-    uint32_t va[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int r = 64 * wave + (lane >> 3) + 8 * i;
-      const int c = (lane & 7) ^ a_swz(r);
-      va[i] = (uint32_t)(((int64_t)min(m0 + r, d.M - 1) * d.lda + c * 8) * 2);
-    }
-    auto dma_a = [&](int stage, int kt) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        uint8_t* dst = lds + stage * kAStage + (64 * wave + 8 * i) * (BK * 2);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)dst, 16, va[i],
-                                                 kt * BK * 2, 0, 0);
-      }
-    };
-
-    // prologue: steps 0 and 1 in flight, step 0's first half decoded
-    dma_a(0, 0);
-    if (active) load_raw(raw[0], 0);
-    if (KT > 1) {
-      dma_a(1, 1);
-      if (active) load_raw(raw[1], 1);
-    }
-    if (active) decode_half(raw[0], 0);
-    wait_vm<0>();
-    __syncthreads();
-
-    auto step = [&]<int S>(int kt) {
-      const bool more = kt + 2 < KT;
-      if (more) {
-        dma_a((S + 2) % 3, kt + 2);
-        if (active) load_raw(raw[(S + 2) % 3], kt + 2);
-      }
-      const uint8_t* st = lds + S * kAStage;
-      if (active) {
-        // one basic block: decode of the other half (VALU) and A reads (LDS) interleaved with the MFMAs; the decode
-        // of the next step's first half runs even on the last step (its result is then unused)
-        decode_half(raw[S], 1);
-        mfma_half(st, aoff0, 0);
-        decode_half(raw[(S + 1) % 3], 0);
-        mfma_half(st, aoff1, 1);
-        interleave_schedule();
-      }
-      // A(kt+1) must have landed before the barrier; the loads issued in this step may stay in flight
-      if (more)
-        wait_vm<16>();
-      else
-        wait_vm<0>();
-      __syncthreads();
-    };
-    int kt = 0;
-    for (; kt + 3 <= KT; kt += 3) {
-      step.template operator()<0>(kt);
-      step.template operator()<1>(kt + 1);
-      step.template operator()<2>(kt + 2);
-    }
-    if (kt < KT) step.template operator()<0>(kt);
-    if (kt + 1 < KT) step.template operator()<1>(kt + 1);
-  } else {
-    // ---- register-staged path (A converted from bf16-with-quantize or packed bytes): B of the next step is loaded
-    // before the MFMAs of this step, A after them; both are converted before the barrier.
-    uint32_t braw[4][2][3];
-    auto load_b = [&](int kt) {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-          const uint32_t* p = reinterpret_cast<const uint32_t*>(bptr[j] + (int64_t)kt * kTileBytes + h * 576);
-          braw[j][h][0] = p[0];
-          braw[j][h][1] = p[1];
-          braw[j][h][2] = p[2];
-        }
-    };
-    auto decode_b = [&]() {
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int h = 0; h < 2; h++) bcur[j][h] = decode_window(braw[j][h][0], braw[j][h][1], braw[j][h][2], bo);
-    };
-    u32x4 av[8];
-    load_a<AFMT>(d, m0, 0, tid, av);
-    if (active) load_b(0);
-    store_a<AFMT>(lds, tid, av);
-    if (active) decode_b();
-    __syncthreads();
-    for (int kt = 0; kt < KT; kt++) {
-      const uint8_t* st = lds + (kt & 1) * kAStage;
-      if (kt + 1 < KT && active) load_b(kt + 1);
-      if (active) {
-        mfma_half(st, aoff0, 0);
-        mfma_half(st, aoff1, 1);
-      }
-      if (kt + 1 < KT) {
-        load_a<AFMT>(d, m0, kt + 1, tid, av);
-        store_a<AFMT>(lds + ((kt + 1) & 1) * kAStage, tid, av);
-        if (active) decode_b();
-      }
-      __syncthreads();
-    }
-  }
-
-  // ---- epilogue: through LDS, 64 rows at a time ----------------------------------------------------------------
-  // Phase A: each wave writes its fp32 accumulators for 64 rows into the row-quad LDS tile (one 16-byte store per
-  // accumulator). Phase B: each thread takes 4 rows x 8 output columns (each row's 8 columns are one bfp16 block when
-  // re-quantizing), applies the epilogue in fp32 and writes 16 bytes of bf16 per row.
-  float* ep = reinterpret_cast<float*>(lds);
-  const int col_in = lane & 15;
-  const bool swiglu = d.act == RL_ACT_SWIGLU;
-  const int nout = swiglu ? N / 2 : N;
-  auto pass = [&]<int P>() {
-    if (active) {
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int c = ep_slot(16 * grp[j] + col_in);
-#pragma unroll
-        for (int f = 0; f < 4; f++)
-          *reinterpret_cast<f32x4*>(ep + ((4 * f + (lane >> 4)) * 256 + c) * 4) = acc[4 * P + f][j];
-      }
-    }
-    __syncthreads();
-    epilogue_rows<kGThreads>(d, ep, m0 + 64 * P, n0, nout, tid);
-    __syncthreads();
-  };
-  pass.template operator()<0>();
-  pass.template operator()<1>();
-  pass.template operator()<2>();
-  pass.template operator()<3>();
 }
 
 // ---- 8-wave kernel for bf16 A ---------------------------------------------------------------------------------
@@ -1417,23 +1048,43 @@ static GemmDesc rows_from(const GemmDesc& g, int64_t R) {
   return t;
 }
 
-template <int G>
-static int launch(const GemmArgs<G>& args, int total_tiles, int32_t a_fmt, void* stream) {
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(total_tiles), block(kGThreads);
-  switch (a_fmt) {
-    case RL_A_BF16_QUANTIZE: hipLaunchKernelGGL((gemm_kernel<RL_A_BF16_QUANTIZE, G>), grid, block, 0, st, args); break;
-    case RL_A_PACKED_ROWBLOCK:
-      hipLaunchKernelGGL((gemm_kernel<RL_A_PACKED_ROWBLOCK, G>), grid, block, 0, st, args);
-      break;
-    default: hipLaunchKernelGGL((gemm_kernel<RL_A_PACKED_A_LAYOUT, G>), grid, block, 0, st, args); break;
-  }
-  return launch_status("rl_bfp16_gemm");
-}
-
 // Bytes of the bf16 A copy that rl_bfp16_gemm_ws stages at the start of the workspace for a non-bf16 A format,
 // rounded up so that the K-split partials after it stay 256-byte aligned.
 static int64_t staged_a_bytes(int64_t M, int64_t K) { return (M * K * 2 + 255) / 256 * 256; }
+
+// Writes A of a non-bf16 format as bf16 into a16 (M x K, row stride K): its bfp16 values, after quantizing along K
+// for RL_A_BF16_QUANTIZE. One HBM-bound pass (9/8 or 2 bytes read and 2 written per value).
+static int stage_a(const void* A, int32_t a_fmt, int64_t lda, int64_t M, int64_t K, uint16_t* a16, void* stream) {
+  if (a_fmt == RL_A_BF16_QUANTIZE)
+    return rl_bfp16_quantize(A, RL_DTYPE_BF16, M, K, lda, RL_ORDER_ROWBLOCK, nullptr, a16, stream);
+  return rl_bfp16_dequantize(static_cast<const uint8_t*>(A),
+                             a_fmt == RL_A_PACKED_A_LAYOUT ? RL_ORDER_A_LAYOUT : RL_ORDER_ROWBLOCK, M, K, a16,
+                             RL_DTYPE_BF16, stream);
+}
+
+// Device memory for a call that was given no workspace: a stream-ordered allocation on the call's stream, released
+// by stream_free once the call's launches are queued. A stream under graph capture is refused (RL_ERR_WORKSPACE):
+// such callers pass a workspace (rl_bfp16_gemm_ws) or use the fixed scratch (rl_bfp16_gemm_noalloc).
+static int stream_alloc(void** p, int64_t bytes, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess) return fail(RL_ERR_DEVICE, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(RL_ERR_WORKSPACE, "a non-bf16 A under stream capture needs a workspace (rl_bfp16_gemm_ws, "
+                                  "rl_bfp16_gemm_workspace_size bytes) or rl_bfp16_gemm_noalloc");
+  e = hipMallocAsync(p, (size_t)bytes, st);
+  if (e != hipSuccess) return fail(RL_ERR_DEVICE, "hipMallocAsync(%lld bytes): %s", (long long)bytes,
+                                   hipGetErrorString(e));
+  return RL_OK;
+}
+
+// Releases a stream_alloc allocation on the same stream; returns the call's status s, or the free's failure.
+static int stream_free(void* p, void* stream, int s) {
+  const hipError_t e = hipFreeAsync(p, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess && s == RL_OK) return fail(RL_ERR_DEVICE, "hipFreeAsync: %s", hipGetErrorString(e));
+  return s;
+}
 
 }  // namespace rl
 
@@ -1468,21 +1119,22 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
   args.n = 1;
   if ((s = check_device())) return s;
   if (a_fmt != RL_A_BF16) {
-    if (!workspace) return launch<1>(args, args.d[0].tiles_m * args.d[0].tiles_n, a_fmt, stream);
-    // stage A as bf16 (its bfp16 values) at the start of the workspace in one HBM-bound pass, then run the bf16
-    // path with the rest of the workspace
+    if (!workspace) {
+      // no workspace: the same call on a stream-ordered allocation of the size this format and shape use
+      const int64_t need = rl_bfp16_gemm_workspace_size(a_fmt, M, N, K);
+      void* tmp = nullptr;
+      if ((s = stream_alloc(&tmp, need, stream))) return s;
+      s = rl_bfp16_gemm_ws(A, a_fmt, lda, B_packed, C, ldc, M, N, K, ep, tmp, need, stream);
+      return stream_free(tmp, stream, s);
+    }
+    // stage A as bf16 (its bfp16 values) at the start of the workspace, then run the bf16 path with the rest of
+    // the workspace
     const int64_t sa = staged_a_bytes(M, K);
     if (workspace_bytes < sa)
       return fail(RL_ERR_WORKSPACE, "workspace %lld bytes, staging A needs %lld (rl_bfp16_gemm_workspace_size)",
                   (long long)workspace_bytes, (long long)sa);
     uint16_t* a16 = static_cast<uint16_t*>(workspace);
-    if (a_fmt == RL_A_BF16_QUANTIZE)
-      s = rl_bfp16_quantize(A, RL_DTYPE_BF16, M, K, lda, RL_ORDER_ROWBLOCK, nullptr, a16, stream);
-    else
-      s = rl_bfp16_dequantize(static_cast<const uint8_t*>(A),
-                              a_fmt == RL_A_PACKED_A_LAYOUT ? RL_ORDER_A_LAYOUT : RL_ORDER_ROWBLOCK, M, K, a16,
-                              RL_DTYPE_BF16, stream);
-    if (s) return s;
+    if ((s = stage_a(A, a_fmt, lda, M, K, a16, stream))) return s;
     const int64_t rest = workspace_bytes - sa;
     return rl_bfp16_gemm_ws(a16, RL_A_BF16, K, B_packed, C, ldc, M, N, K, ep,
                             rest > 0 ? static_cast<uint8_t*>(workspace) + sa : nullptr, rest, stream);
@@ -1602,7 +1254,26 @@ int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, v
   args.n = n;
   int s = check_device();
   if (s) return s;
-  if (a_fmt != RL_A_BF16) return launch<RL_MAX_GROUP>(args, total, a_fmt, stream);
+  if (a_fmt != RL_A_BF16) {
+    // stage every member's A as bf16 in one stream-ordered allocation, then run the group on the bf16 path
+    int64_t off[RL_MAX_GROUP], bytes = 0;
+    for (int i = 0; i < n; i++) {
+      off[i] = bytes;
+      bytes += staged_a_bytes(descs[i].M, descs[i].K);
+    }
+    void* tmp = nullptr;
+    if ((s = stream_alloc(&tmp, bytes, stream))) return s;
+    rl_gemm_desc staged[RL_MAX_GROUP];
+    for (int i = 0; i < n && !s; i++) {
+      staged[i] = descs[i];
+      staged[i].A = static_cast<uint8_t*>(tmp) + off[i];
+      staged[i].lda = descs[i].K;
+      s = stage_a(descs[i].A, a_fmt, descs[i].lda, descs[i].M, descs[i].K,
+                  static_cast<uint16_t*>(const_cast<void*>(staged[i].A)), stream);
+    }
+    if (!s) s = rl_bfp16_gemm_grouped(staged, n, RL_A_BF16, stream);
+    return stream_free(tmp, stream, s);
+  }
   // one launch for the whole group, with the fragment count that minimises its rounds
   const int cus = device_cus();
   int best_mf = 8;

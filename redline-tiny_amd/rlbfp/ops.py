@@ -155,12 +155,13 @@ def staged_a_bytes(M, K):
 
 
 def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None, gate_split_row=0,
-         residual=None, quantize_out=False, out=None, split=True, stage=True):
+         residual=None, quantize_out=False, out=None, split=True, workspace=True):
     """C = epilogue(A @ B) with B the packed weight stream of a (K, N) matrix, bf16 output (M, N) (or (M, N/2) for
     act="swiglu"). See rl_bfp16_gemm in include/rlbfp.h for the epilogue order. split: let a small-M, deep-K GEMM
-    split K into pieces (rl_bfp16_gemm_ws, workspace from torch's allocator); False: always whole K. stage: for an
-    A format other than "bf16", decode (or quantize) A into a bf16 copy in the workspace first and run the bf16
-    kernel; False: the register-staged kernel reads the format directly (slower)."""
+    split K into pieces (rl_bfp16_gemm_ws, workspace from torch's allocator); False: always whole K. An A format
+    other than "bf16" is decoded (or quantized) into a bf16 copy first, then the bf16 kernel runs; workspace: that
+    copy (and any K split) lives in a workspace from torch's allocator; False: rl_bfp16_gemm takes a stream-ordered
+    allocation of its own (not allowed under graph capture)."""
     _dev(a, "A")
     _dev(b_packed, "B")
     if M is None:
@@ -177,12 +178,12 @@ def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None
         raise ValueError(f"out must be ({M}, {nout}) bfloat16 with unit column stride")
     _check_ep_sizes(M, N, nout, bias, gate, gate_split_row, residual)
     ep = _epilogue(act, bias, gate, gate_split_row, residual, quantize_out)
-    if a_fmt == "bf16":
-        nws = gemm_workspace_bytes(M, N, K, a.device) if split else 0
-    elif stage:
-        nws = gemm_workspace_bytes(M, N, K, a.device, a_fmt) if split else staged_a_bytes(M, K)
-    else:
+    if not workspace:
         nws = 0
+    elif a_fmt == "bf16":
+        nws = gemm_workspace_bytes(M, N, K, a.device) if split else 0
+    else:
+        nws = gemm_workspace_bytes(M, N, K, a.device, a_fmt) if split else staged_a_bytes(M, K)
     if nws:
         ws = torch.empty(nws, dtype=torch.uint8, device=a.device)
         L.check(L.lib().rl_bfp16_gemm_ws(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M,
@@ -194,15 +195,16 @@ def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None
 
 
 class GemmSpec:
-    """One GEMM of a grouped launch (same arguments as gemm(); A is bf16 for every member)."""
+    """One GEMM of a grouped launch (same arguments as gemm()); A is in the group's format (gemm_grouped's a_fmt),
+    and M is required when that format is packed."""
 
     def __init__(self, a, b_packed, N, K, act=None, bias=None, gate=None, gate_split_row=0, residual=None,
-                 quantize_out=False, out=None):
+                 quantize_out=False, out=None, M=None):
         self.a, self.b, self.N, self.K = a, b_packed, N, K
+        self.M = a.shape[0] if M is None else M
         self.ep_args = (act, bias, gate, gate_split_row, residual, quantize_out)
         nout = N // 2 if act == "swiglu" else N
-        self.out = out if out is not None else torch.empty((a.shape[0], nout), dtype=torch.bfloat16,
-                                                           device=a.device)
+        self.out = out if out is not None else torch.empty((self.M, nout), dtype=torch.bfloat16, device=a.device)
 
 
 def gemm_grouped(specs, a_fmt="bf16"):
@@ -213,7 +215,7 @@ def gemm_grouped(specs, a_fmt="bf16"):
     keep = []
     for i, s in enumerate(specs):
         _dev(s.a, "A")
-        M = s.a.shape[0]
+        M = s.M
         arr[i].A = s.a.data_ptr()
         arr[i].lda = _a_args(s.a, a_fmt, M, s.K)
         arr[i].B_packed = s.b.data_ptr()

@@ -59,11 +59,11 @@ def test_output_canary_and_ldc(dev):
     assert (big[:, N:] == 7.0).all() and (big[M:, :] == 7.0).all()
 
 
-@pytest.mark.parametrize("stage", [True, False])
+@pytest.mark.parametrize("workspace", [True, False])
 @pytest.mark.parametrize("a_fmt", ["bf16_quantize", "packed_rowblock", "packed_a_layout"])
-def test_a_formats_agree(dev, a_fmt, stage):
-    """Every A format computes on the same bfp16 values: results identical to the bf16 (pre-quantized) path, whether A
-    is staged as bf16 in the workspace first (stage) or read by the register-staged kernel."""
+def test_a_formats_agree(dev, a_fmt, workspace):
+    """Every A format computes on the same bfp16 values: results identical to the bf16 (pre-quantized) path, whether
+    the staged bf16 copy of A lives in the caller's workspace or in the library's own stream-ordered allocation."""
     M, K, N = 256, 192, 256
     rng, A, packed, Aq, Bq = setup(M, K, N, 4, outliers=0.01)
     b = dev_t(packed, torch.uint8)
@@ -74,7 +74,7 @@ def test_a_formats_agree(dev, a_fmt, stage):
         a = dev_t(F.to_bfp16(A.reshape(-1)), torch.uint8)
     else:
         a = dev_t(F.to_bfp16(F.a_layout(A)), torch.uint8)
-    got = ops.gemm(a, b, N, K, M=M, a_fmt=a_fmt, stage=stage)
+    got = ops.gemm(a, b, N, K, M=M, a_fmt=a_fmt, workspace=workspace)
     assert torch.equal(got, ref)
     check(got, G.gemm_ref(Aq, Bq))
 
@@ -169,6 +169,22 @@ def test_grouped_matches_single(dev):
         refs.append(ops.gemm(a, b, N, K, act=act))
     outs = ops.gemm_grouped(specs)
     for o, r in zip(outs, refs):
+        assert torch.equal(o, r)
+
+
+@pytest.mark.parametrize("a_fmt", ["packed_a_layout", "bf16_quantize"])
+def test_grouped_non_bf16_a(dev, a_fmt):
+    """A grouped launch with A in another format (every member's A staged as bf16 in one allocation first) gives the
+    bits of the bf16-A group on the quantized values."""
+    rng = np.random.default_rng(10)
+    specs, specs16 = [], []
+    for M, K, N, act in ((256, 128, 384, None), (128, 192, 256, "swiglu")):
+        A = G.activations(rng, M, K)
+        b = dev_t(F.pack_b(G.linear_weight(rng, N, K).T), torch.uint8)
+        a = dev_t(F.to_bfp16(F.a_layout(A)), torch.uint8) if a_fmt == "packed_a_layout" else dev_t(A, torch.bfloat16)
+        specs.append(ops.GemmSpec(a, b, N, K, act=act, M=M))
+        specs16.append(ops.GemmSpec(dev_t(F.quantize_rows(A), torch.bfloat16), b, N, K, act=act))
+    for o, r in zip(ops.gemm_grouped(specs, a_fmt=a_fmt), ops.gemm_grouped(specs16)):
         assert torch.equal(o, r)
 
 

@@ -591,6 +591,7 @@ constexpr int kW4GroupM = 2;           // M-tiles per group in an XCD's tile ran
 
 template <int G, int MF>
 __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G> args) {
+  static_assert(MF >= 4 && MF <= 8, "four decode octets per phase, 8 x 8 accumulators at most");
   constexpr int TM = 64 * MF;       // tile rows: 16 MF per wave, four waves down
   constexpr int kAS = TM * BK * 2;  // bytes of one A stage
   constexpr int kDma = TM / 32;     // A loads of 8 rows per wave per stage
@@ -708,8 +709,8 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
   // One phase in octets (row fragment mf: its 8 MFMAs, then the next phase's fragment mf read into the same
   // registers), scheduling fences between octets. The next phase's B fragments are read one per octet (the last
   // octet reads what MF < 8 leaves), so LDS reads never come in bursts. P = 0 also decodes raw B(k+1) into stage ds
-  // (block J in octet J) and issues the three loads of raw B(kl) in octets 4..6 (MF = 6: 3..5); P = 1 issues the
-  // DMA of A(kl) into A stage sa, two loads per octet.
+  // (block J in octet J) and issues the three loads of raw B(kl) in octets 4..6 (MF = 6: 3..5; MF = 4: all in the
+  // last octet); P = 1 issues the DMA of A(kl) into A stage sa, two loads per octet.
   auto phase = [&]<int P>(bf16x8(&cur)[8], bf16x8(&nxt)[8], const uint8_t* na, const uint8_t* nb, uint8_t* ds, int kl,
                           int sa) {
     constexpr int kRaw0 = MF >= 7 ? 4 : 3;
@@ -728,7 +729,13 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
         if (mf == 1) decode_store.template operator()<1>(ds);
         if (mf == 2) decode_store.template operator()<2>(ds);
         if (mf == 3) decode_store.template operator()<3>(ds);
-        if (mf >= kRaw0 && mf < kRaw0 + 3) load_raw(kl, mf - kRaw0);
+        if constexpr (MF >= 6) {
+          if (mf >= kRaw0 && mf < kRaw0 + 3) load_raw(kl, mf - kRaw0);
+        } else if (mf == MF - 1) {  // MF = 4, 5: all three after the last decode
+          load_raw(kl, 0);
+          load_raw(kl, 1);
+          load_raw(kl, 2);
+        }
         constexpr int kMfma = 0x008, kValu = 0x002, kDsWrite = 0x200;
         if (mf < 4) {
 #pragma unroll
@@ -885,9 +892,9 @@ static Plan8 plan8(int64_t M, int64_t N, int cus) {
 // (a 256 x 256 tile of MF = 8 costs 9.5): per round of the CUs it runs ~6% faster than the 8-wave kernel on the same
 // FLOPs, because it decodes half the B blocks per MFMA and reads a third fewer operand bytes from LDS (measured on
 // the DiT FFN shapes, bit-identical results). Its last M-tile may be partial. The plan is one launch, or a first
-// launch over rows [0, split) and a second one of the 8-wave kernel over the rest.
+// launch over rows [0, split) and a second one, of either kernel, over the rest (GELU: the 8-wave kernel only).
 constexpr double kTileFixed4 = 0.9;
-constexpr int kMf4Choices[] = {8, 7, 6};
+constexpr int kMf4Choices[] = {8, 7, 6, 4};
 
 static int64_t tiles4(int64_t M, int64_t N, int mf) { return ((M + 64 * mf - 1) / (64 * mf)) * (N / 128); }
 static double launch_cost4(int64_t tiles, int mf, int cus) {
@@ -898,7 +905,8 @@ struct PlanG {
   bool w4;        // the first launch runs the 4-wave kernel
   int mf;         // its fragment count
   int64_t split;  // rows of the first launch; 0 = one launch over all rows
-  int mf_tail;    // fragments per wave of the 8-wave second launch
+  bool tail_w4;   // the second launch runs the 4-wave kernel
+  int mf_tail;    // its fragment count
 };
 
 // RLBFP_GEMM_KERNEL=4w or 8w restricts the plan to plans whose first launch runs that kernel (for A/B measurements).
@@ -911,17 +919,24 @@ static int kernel_restriction() {
   return v;
 }
 
-static PlanG plan_gemm(int64_t M, int64_t N, int cus, int act) {
+static PlanG plan_gemm(int64_t M, int64_t N, int cus, int act, double* cost = nullptr) {
   // the tanh GELU epilogue's transcendentals cost more on one wave per SIMD than they save in the main loop
   // (measured at 4096 x 3072 x 3072: 102 against 97 us), so GELU stays on the 8-wave kernel unless forced
   const int only = kernel_restriction() ? kernel_restriction() : (act == RL_ACT_GELU_TANH ? 2 : 0);
-  PlanG best{false, 8, 0, 8};
+  PlanG best{false, 8, 0, false, 8};
   double bc = 1e300;
-  auto best_tail = [&](int64_t rows, int& mf_out) {
+  // the cheapest launch over `rows` rows: the 8-wave kernel, or (unless GELU) the 4-wave one
+  auto best_tail = [&](int64_t rows, bool& w4_out, int& mf_out) {
     double c = 1e300;
     for (int mf : kMfChoices) {
       const double t = launch_cost(tiles8(rows, N, mf), mf, cus);
-      if (t < c) { c = t; mf_out = mf; }
+      if (t < c) { c = t; w4_out = false; mf_out = mf; }
+    }
+    if (act != RL_ACT_GELU_TANH) {
+      for (int mf : kMf4Choices) {
+        const double t = launch_cost4(tiles4(rows, N, mf), mf, cus);
+        if (t < c) { c = t; w4_out = true; mf_out = mf; }
+      }
     }
     return c;
   };
@@ -930,19 +945,21 @@ static PlanG plan_gemm(int64_t M, int64_t N, int cus, int act) {
     double c = launch_cost(tiles8(p.split ? p.split : M, N, p.mf), p.mf, cus);
     if (p.split) c += kSecondLaunch + launch_cost(tiles8(M - p.split, N, p.mf_tail), p.mf_tail, cus);
     bc = c;
-    best = PlanG{false, p.mf, p.split, p.mf_tail};
+    best = PlanG{false, p.mf, p.split, false, p.mf_tail};
   }
   if (only != 2) {
     for (int mf : kMf4Choices) {
       const double c = launch_cost4(tiles4(M, N, mf), mf, cus);
-      if (c < bc) { bc = c; best = PlanG{true, mf, 0, 8}; }
+      if (c < bc) { bc = c; best = PlanG{true, mf, 0, false, 8}; }
       for (int64_t R = 64 * mf; R < M; R += 64 * mf) {
+        bool tw = false;
         int mt = 8;
-        const double c2 = launch_cost4(tiles4(R, N, mf), mf, cus) + kSecondLaunch + best_tail(M - R, mt);
-        if (c2 < bc) { bc = c2; best = PlanG{true, mf, R, mt}; }
+        const double c2 = launch_cost4(tiles4(R, N, mf), mf, cus) + kSecondLaunch + best_tail(M - R, tw, mt);
+        if (c2 < bc) { bc = c2; best = PlanG{true, mf, R, tw, mt}; }
       }
     }
   }
+  if (cost) *cost = bc;
   return best;
 }
 
@@ -1032,7 +1049,8 @@ static int launch4w(const GemmArgs<G>& args, int total_tiles, int mf, void* stre
   switch (mf) {
     case 8: hipLaunchKernelGGL((gemm4w_kernel<G, 8>), grid, block, 0, st, args); break;
     case 7: hipLaunchKernelGGL((gemm4w_kernel<G, 7>), grid, block, 0, st, args); break;
-    default: hipLaunchKernelGGL((gemm4w_kernel<G, 6>), grid, block, 0, st, args); break;
+    case 6: hipLaunchKernelGGL((gemm4w_kernel<G, 6>), grid, block, 0, st, args); break;
+    default: hipLaunchKernelGGL((gemm4w_kernel<G, 4>), grid, block, 0, st, args); break;
   }
   return launch_status("rl_bfp16_gemm");
 }
@@ -1046,6 +1064,32 @@ static GemmDesc rows_from(const GemmDesc& g, int64_t R) {
   t.M = (int32_t)(g.M - R);
   t.gate_split = (int32_t)(g.gate_split > R ? g.gate_split - R : 0);
   return t;
+}
+
+// One whole-K GEMM (a filled descriptor, bf16 A) as the plan's one or two launches.
+static int launch_planned(const GemmDesc& g, const PlanG& p, void* stream) {
+  GemmArgs<1> args, tail;
+  args.d[0] = g;
+  args.n = tail.n = 1;
+  if (p.split) {
+    tail.d[0] = rows_from(g, p.split);
+    args.d[0].M = (int32_t)p.split;
+  }
+  int total = 0, s;
+  if (p.w4) {
+    set_tiles4w(args, p.mf, total);
+    s = launch4w<1>(args, total, p.mf, stream);
+  } else {
+    set_tiles8(args, p.mf, total);
+    s = launch8<1>(args, total, p.mf, stream);
+  }
+  if (s || !p.split) return s;
+  if (p.tail_w4) {
+    set_tiles4w(tail, p.mf_tail, total);
+    return launch4w<1>(tail, total, p.mf_tail, stream);
+  }
+  set_tiles8(tail, p.mf_tail, total);
+  return launch8<1>(tail, total, p.mf_tail, stream);
 }
 
 // Bytes of the bf16 A copy that rl_bfp16_gemm_ws stages at the start of the workspace for a non-bf16 A format,
@@ -1156,23 +1200,7 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
       return launch_status("rl_bfp16_gemm (reduce)");
     }
   }
-  const PlanG p = plan_gemm(M, N, device_cus(), ep ? ep->act : RL_ACT_NONE);
-  GemmArgs<1> tail;
-  if (p.split) {
-    tail.d[0] = rows_from(args.d[0], p.split);
-    tail.n = 1;
-    args.d[0].M = (int32_t)p.split;
-  }
-  if (p.w4) {
-    set_tiles4w(args, p.mf, total);
-    s = launch4w<1>(args, total, p.mf, stream);
-  } else {
-    set_tiles8(args, p.mf, total);
-    s = launch8<1>(args, total, p.mf, stream);
-  }
-  if (s || !p.split) return s;
-  set_tiles8(tail, p.mf_tail, total);
-  return launch8<1>(tail, total, p.mf_tail, stream);
+  return launch_planned(args.d[0], plan_gemm(M, N, device_cus(), ep ? ep->act : RL_ACT_NONE), stream);
 }
 
 int rl_bfp16_gemm(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B_packed, uint16_t* C, int64_t ldc,
@@ -1274,7 +1302,12 @@ int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, v
     if (!s) s = rl_bfp16_gemm_grouped(staged, n, RL_A_BF16, stream);
     return stream_free(tmp, stream, s);
   }
-  // one launch for the whole group, with the fragment count that minimises its rounds
+  // one 8-wave launch for the whole group, with the fragment count that minimises its rounds; or, when the model
+  // puts it lower, each member as its own planned launches (e.g. the SwiGLU up GEMMs of the image and text streams:
+  // the 4-wave kernel's 512-row tiles over the 4096 image rows and 256-row tiles over the 256 text rows, where one
+  // launch would round both to 256-row tiles of the 8-wave kernel). The 4-wave kernel is not used for the single
+  // launch: with members of different weights it measured slower than the 8-wave one (627-646 against 619 us for
+  // the two up GEMMs, 299-306 against 280 us for the two QKV GEMMs).
   const int cus = device_cus();
   int best_mf = 8;
   double bc = 1e300;
@@ -1283,6 +1316,18 @@ int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, v
     for (int i = 0; i < n; i++) t += tiles8(args.d[i].M, args.d[i].N, mf);
     const double c = launch_cost(t, mf, cus);
     if (c < bc) { bc = c; best_mf = mf; }
+  }
+  PlanG plans[RL_MAX_GROUP];
+  double each = kSecondLaunch * (n - 1);
+  for (int i = 0; i < n; i++) {
+    double c = 0;
+    plans[i] = plan_gemm(args.d[i].M, args.d[i].N, cus, args.d[i].act, &c);
+    each += c;
+  }
+  if (each < bc) {
+    for (int i = 0; i < n; i++)
+      if ((s = launch_planned(args.d[i], plans[i], stream))) return s;
+    return RL_OK;
   }
   set_tiles8(args, best_mf, total);
   return launch8<RL_MAX_GROUP>(args, total, best_mf, stream);

@@ -777,17 +777,26 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
 #pragma unroll
   for (int j = 0; j < 8; j++) bj[j] = d.bias ? d.bias[n0 + 16 * j + col_in] : 0.f;
   if (swiglu) {
+    // without a bias (the FFN up GEMMs) the two adds per output are left out of this transcendental-bound pass
+    auto swiglu_pass = [&]<bool kBias>() {
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const int c = ep_slot(16 * g + col_in);
+      for (int g = 0; g < 4; g++) {
+        const int c = ep_slot(16 * g + col_in);
 #pragma unroll
-      for (int mf = 0; mf < MF; mf++) {
-        f32x4 v;
+        for (int mf = 0; mf < MF; mf++) {
+          f32x4 v;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = silu_f(acc[mf][g][i] + bj[g]) * (acc[mf][g + 4][i] + bj[g + 4]);
-        *reinterpret_cast<f32x4*>(ep + ((4 * MF * wave + 4 * mf + (lane >> 4)) * 64 + c) * 4) = v;
+          for (int i = 0; i < 4; i++)
+            v[i] = kBias ? silu_f(acc[mf][g][i] + bj[g]) * (acc[mf][g + 4][i] + bj[g + 4])
+                         : silu_f(acc[mf][g][i]) * acc[mf][g + 4][i];
+          *reinterpret_cast<f32x4*>(ep + ((4 * MF * wave + 4 * mf + (lane >> 4)) * 64 + c) * 4) = v;
+        }
       }
-    }
+    };
+    if (d.bias)
+      swiglu_pass.template operator()<true>();
+    else
+      swiglu_pass.template operator()<false>();
     __syncthreads();
     ep8_finish<64, kW4Threads>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
   } else {

@@ -169,8 +169,10 @@ __device__ __forceinline__ BlockScale block_scales(uint32_t E) {
   return BlockScale{__uint_as_float((260u - E) << 23), __uint_as_float(0x42FE0000u + ((E - 133u) << 23)),
                     __uint_as_float((E - 6u) << 23)};
 }
+// min(x, t) as one v_med3_f32 against -FLT_MAX: x is finite here, so no NaN quieting is needed (fminf would add a
+// canonicalising v_max of each operand)
 __device__ __forceinline__ float encode_fast(float x, const BlockScale& k) {
-  return __builtin_fmaf(fminf(x, k.t), k.s, kMagic);
+  return __builtin_fmaf(__builtin_amdgcn_fmed3f(x, -3.402823466e38f, k.t), k.s, kMagic);
 }
 // Decoded value of an encode_fast result: f * 2^(E-133) is exact, and adding -1.5 * 2^23 * 2^(E-133) leaves
 // q * 2^(E-133), representable, so the fma does not round (+0 for q = 0)

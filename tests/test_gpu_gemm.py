@@ -343,3 +343,34 @@ def test_weight_block_exponents(dev, classes, a_scale):
             continue
         assert np.abs(got - want).max() <= TOL * scale, (n, classes[n % len(classes)])
         assert (np.abs(got - want) <= 2 * np.abs(want) * 2.0 ** -8 + 1e-4 * scale).mean() > 0.99, n
+
+
+def test_packed_a_without_workspace_refused_under_capture(dev):
+    """A non-bf16 A with no workspace stages into a stream-ordered allocation, which a stream under graph capture
+    cannot take: the call is refused with RL_ERR_WORKSPACE before anything is enqueued, and the same call with a
+    workspace is captured and replays to the eager result."""
+    from rlbfp import _lib as L
+    M, K, N = 128, 128, 256
+    rng, A, packed, Aq, Bq = setup(M, K, N, 11)
+    a = dev_t(F.to_bfp16(F.a_layout(A)), torch.uint8)
+    b = dev_t(packed, torch.uint8)
+    ref = ops.gemm(a, b, N, K, M=M, a_fmt="packed_a_layout", workspace=False)
+    out = torch.zeros_like(ref)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        try:
+            with pytest.raises(L.RLError) as e:
+                ops.gemm(a, b, N, K, M=M, a_fmt="packed_a_layout", workspace=False, out=out)
+            ops.gemm(a, b, N, K, M=M, a_fmt="packed_a_layout", out=out)
+        finally:
+            graph.capture_end()
+    assert e.value.code == L.RL_ERR_WORKSPACE
+    torch.cuda.current_stream().wait_stream(side)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)

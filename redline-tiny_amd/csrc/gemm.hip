@@ -78,11 +78,30 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
 // path (encode_fast / decode_fast: one exact power-of-two scaling and one half-to-even rounding per value) for block
 // exponents 8..237, the integer encoder otherwise, so the result equals the integer encoder's and does not depend on
 // the denormal mode. -0 comes back as +0, as from_bfp16 gives it.
-__device__ __forceinline__ u32x4 requantize8(u32x4 o) {
+__device__ __forceinline__ uint32_t block_exp8(u32x4 o) {
   const uint32_t w[4] = {o.x, o.y, o.z, o.w};
   uint32_t E = 0;
 #pragma unroll
   for (int k = 0; k < 4; k++) E = max(E, max((w[k] >> 7) & 0xFFu, (w[k] >> 23) & 0xFFu));
+  return E;
+}
+// the fast path of requantize8 for a block whose exponent E is in kFastEMin..kFastEMax
+__device__ __forceinline__ u32x4 requantize8_fast(u32x4 o, uint32_t E) {
+  const uint32_t w[4] = {o.x, o.y, o.z, o.w};
+  const BlockScale sc = block_scales(E);
+  const float off = -kMagic * sc.inv;
+  uint32_t r[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const float lo = decode_fast(encode_fast(__uint_as_float(w[k] << 16), sc), sc, off);
+    const float hi = decode_fast(encode_fast(__uint_as_float(w[k] & 0xFFFF0000u), sc), sc, off);
+    r[k] = pack_hi(lo, hi);
+  }
+  return u32x4{r[0], r[1], r[2], r[3]};
+}
+__device__ __forceinline__ u32x4 requantize8(u32x4 o) {
+  const uint32_t w[4] = {o.x, o.y, o.z, o.w};
+  const uint32_t E = block_exp8(o);
   if (E < kFastEMin || E > kFastEMax) return quantize_bf16x8(o);
   const BlockScale sc = block_scales(E);
   const float off = -kMagic * sc.inv;
@@ -128,31 +147,99 @@ __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int oc
   return o;
 }
 
-// Second half of the 8-wave kernel's epilogue. The LDS tile holds fp32 values (bias, activation and the SwiGLU
-// product already applied) of `nquads` row quads x W staged columns in the row-quad layout; staged column c is output
-// column c0 + c. Each thread takes blocks of 4 rows x 8 columns: gate / residual, bf16 rounding, optional
-// re-quantize, one 16-byte store per row.
+// Gate / residual, bf16 rounding and the optional re-quantize of rows row0..row0+3 of one 8-column block (v[i]:
+// row i's values), as finish_block does for one row. All four rows are computed, rows past M on the last valid row's
+// operands (the caller does not store them), and the re-quantize takes its float fast path for all four at once when
+// every lane's blocks allow it (a wave-uniform test): the rows' dependency chains then interleave, which a wave with
+// no other wave on its SIMD needs.
+__device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int ocol, int nout, float (&v)[4][8],
+                                             u32x4 (&o)[4]) {
+  if (d.gate || d.res) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = min(row0 + i, d.M - 1);
+      const float* g = d.gate ? d.gate + (row < d.gate_split ? nout : 0) + ocol : nullptr;
+      u32x4 r = {0u, 0u, 0u, 0u};
+      if (d.res) r = *reinterpret_cast<const u32x4*>(d.res + (int64_t)row * d.ldr + ocol);
+      const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const float gk = g ? g[k] : 1.0f;
+        const float rk = __uint_as_float(k & 1 ? rw[k >> 1] & 0xFFFF0000u : rw[k >> 1] << 16);
+        v[i][k] = rk + gk * v[i][k];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    o[i] = u32x4{pack_bf16_rne(v[i][0], v[i][1]), pack_bf16_rne(v[i][2], v[i][3]), pack_bf16_rne(v[i][4], v[i][5]),
+                 pack_bf16_rne(v[i][6], v[i][7])};
+  if (d.flags & RL_EP_QUANTIZE_OUT) {
+    uint32_t E[4];
+    bool slow = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      E[i] = block_exp8(o[i]);
+      slow |= E[i] < kFastEMin || E[i] > kFastEMax;
+    }
+    if (__builtin_amdgcn_ballot_w64(slow) == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] = requantize8_fast(o[i], E[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] = requantize8(o[i]);
+    }
+  }
+}
+
+// Second half of the GEMM epilogue. The LDS tile holds fp32 values (bias, activation and the SwiGLU product already
+// applied) of `nquads` row quads x W staged columns in the row-quad layout; staged column c is output column c0 + c.
+// Each thread takes blocks of 4 rows x 8 columns, one 16-byte store per row (the 4-wave kernel: finish_rows4).
 template <int W, int NTH = kG8ThreadsDecl>
 __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, int r0, int c0, int nquads, int nout,
                                           int tid) {
   constexpr int kBlocks = W / 8;
+  if constexpr (NTH == kG8ThreadsDecl) {
+    // the 8-wave kernel (two waves per SIMD, 256 registers each): one row at a time, which fits its registers; the
+    // other wave on the SIMD hides the latencies
+    for (int it = tid; it < nquads * kBlocks; it += NTH) {
+      const int q = it / kBlocks, cb = it % kBlocks;
+      const int col = c0 + 8 * cb;
+      if (col >= nout) continue;
+      f32x4 a[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * W + ep_slot(8 * cb + k)) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = r0 + 4 * q + i;
+        if (row >= d.M) break;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = a[k][i];
+        const u32x4 o = finish_block(d, row, col, nout, v);
+        *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
+      }
+    }
+    return;
+  }
   for (int it = tid; it < nquads * kBlocks; it += NTH) {
     const int q = it / kBlocks, cb = it % kBlocks;
     const int col = c0 + 8 * cb;
-    if (col >= nout) continue;
+    const int row0 = r0 + 4 * q;
+    if (col >= nout || row0 >= d.M) continue;
     f32x4 a[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * W + ep_slot(8 * cb + k)) * 4);
+    float v[4][8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int row = r0 + 4 * q + i;
-      if (row >= d.M) break;
-      float v[8];
+    for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = a[k][i];
-      const u32x4 o = finish_block(d, row, col, nout, v);
-      *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
-    }
+      for (int k = 0; k < 8; k++) v[i][k] = a[k][i];
+    u32x4 o[4];
+    finish_rows4(d, row0, col, nout, v, o);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (row0 + i < d.M) *reinterpret_cast<u32x4*>(d.C + (int64_t)(row0 + i) * d.ldc + col) = o[i];
   }
 }
 
@@ -800,24 +887,33 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
     __syncthreads();
     ep8_finish<64, kW4Threads>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
   } else {
+    // bias and GELU chosen once per tile, so the staging loop has no per-value branches
+    auto stage_pass = [&]<bool kBias, bool kGelu>() {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int c = ep_slot(16 * j + col_in);
+#pragma unroll
+        for (int mf = 0; mf < MF; mf++) {
+          f32x4 v;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            v[i] = kBias ? acc[mf][j][i] + bj[j] : acc[mf][j][i];
+            if (kGelu) v[i] = gelu_tanh_f(v[i]);
+          }
+          *reinterpret_cast<f32x4*>(ep + ((4 * MF * (wave & 1) + 4 * mf + (lane >> 4)) * 128 + c) * 4) = v;
+        }
+      }
+    };
     const bool gelu = d.act == RL_ACT_GELU_TANH;
 #pragma unroll
     for (int P = 0; P < 2; P++) {
       if ((wave >> 1) == P) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int c = ep_slot(16 * j + col_in);
-#pragma unroll
-          for (int mf = 0; mf < MF; mf++) {
-            f32x4 v;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-              v[i] = acc[mf][j][i] + bj[j];
-              if (gelu) v[i] = gelu_tanh_f(v[i]);
-            }
-            *reinterpret_cast<f32x4*>(ep + ((4 * MF * (wave & 1) + 4 * mf + (lane >> 4)) * 128 + c) * 4) = v;
-          }
-        }
+        if (gelu)
+          stage_pass.template operator()<true, true>();
+        else if (d.bias)
+          stage_pass.template operator()<true, false>();
+        else
+          stage_pass.template operator()<false, false>();
       }
       __syncthreads();
       ep8_finish<128, kW4Threads>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);

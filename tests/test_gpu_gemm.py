@@ -208,10 +208,14 @@ def test_config1_full_size_rows(dev):
     check(out[torch.from_numpy(rows).cuda()], G.gemm_ref(Aq, Bq))
 
 
-# Shapes that the launch planner of the bf16 path (256 CUs) runs with 6, 7 and 8 fragment rows per wave (192-, 224-
-# and 256-row tiles), and as a 256-row-tile launch over the first 4096 rows followed by a 128-row-tile launch over
-# the rest. Checked on sampled rows (the first and last tiles and both sides of every tile boundary near the split).
-@pytest.mark.parametrize("M,N", [(3072, 4096), (4352, 3072), (4096, 4096), (4352, 24576)])
+# Shapes that the launch planner of the bf16 path (256 CUs) runs as one launch of the 4-wave kernel with 6, 7 and 8
+# fragment rows per wave (384-, 448- and 512-row tiles) or of the 8-wave kernel (1100 x 24576: 224-row tiles), and as
+# a first 4-wave launch followed by a second launch over the remaining rows: of 256-row 4-wave tiles (4352 and 4296 x
+# 24576, the latter with a partial last tile) or of the 8-wave kernel (4200 x 9216). Checked on sampled rows (the
+# first and last tiles and both sides of every tile boundary near the split), with the gate-row split inside the
+# second launch.
+@pytest.mark.parametrize("M,N", [(3072, 4096), (4352, 3072), (4096, 4096), (4352, 24576), (4296, 24576),
+                                 (4200, 9216), (1100, 24576)])
 def test_tile_plans(dev, M, N):
     K = 64
     rng, A, packed, Aq, Bq = setup(M, K, N, M + N)

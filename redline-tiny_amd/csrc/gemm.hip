@@ -935,6 +935,8 @@ static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, 
   if ((uintptr_t)C % 16) return fail(RL_ERR_ALIGN, "C must be 16-byte aligned");
   if (K * N / 8 * 9 > INT32_MAX || (M - 1) * lda * 2 + K * 2 > INT32_MAX || M * K / 8 * 9 > INT32_MAX)
     return fail(RL_ERR_SHAPE, "an operand is above 2^31 bytes (buffer offsets are 32-bit)");
+  if (a_fmt != RL_A_BF16 && M * K * 2 > INT32_MAX)
+    return fail(RL_ERR_SHAPE, "the bf16 copy of A staged for this format is above 2^31 bytes");
   if (ep && ep->residual && (((uintptr_t)ep->residual % 16) || ep->ld_residual % 8))
     return fail(RL_ERR_ALIGN, "residual must be 16-byte aligned with ld_residual %% 8 == 0");
   if (ep && ep->bias && ((uintptr_t)ep->bias % 4)) return fail(RL_ERR_ALIGN, "bias must be 4-byte aligned");

@@ -185,6 +185,20 @@ def test_gemm_ws_null_pointers_rejected_before_any_gpu_call():
     assert L.lib().rl_bfp16_gemm_ws(None, 0, 64, None, None, 128, 1, 128, 64, None, None, 0, None) == L.RL_ERR_NULL
 
 
+@pytest.mark.parametrize("a_fmt,M,N,K", [
+    (L.RL_A_BF16, 1, 32768, 65536),                 # packed B of 2.4 GB
+    (L.RL_A_BF16, 40000, 128, 32768),               # bf16 A of 2.6 GB
+    (L.RL_A_PACKED_ROWBLOCK, 40000, 128, 32768),    # packed A of 1.5 GB whose staged bf16 copy is 2.6 GB
+])
+def test_gemm_operands_above_2gb_rejected_before_any_gpu_call(a_fmt, M, N, K):
+    """Buffer offsets are 32-bit: an operand (or the staged bf16 copy of a packed A) above 2^31 bytes is refused with
+    RL_ERR_SHAPE while the arguments are checked, before the device is touched (the pointers are never read)."""
+    A, B, C = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000), ctypes.c_void_p(0x30000)
+    lda = K if a_fmt == L.RL_A_BF16 else 0
+    assert L.lib().rl_bfp16_gemm(A, a_fmt, lda, B, C, N, M, N, K, None, None) == L.RL_ERR_SHAPE
+    assert b"2^31" in L.lib().rl_last_error()
+
+
 def _has_gpu():
     try:
         import torch

@@ -9,7 +9,7 @@ The metric is the step's GEMM throughput (2MNK summed over both GEMMs, quantize 
 captured once as a HIP graph and replayed (its eager time, launched from Python, is reported beside it). The
 roofline object is for the dominant kernel, the up GEMM (657.13 GFLOP per call), against the dense bf16 MFMA peak; the
 library runs that call as two launches (the 4-wave kernel over rows 0..4095 in 512 x 128 tiles, six full rounds of the
-256 CUs, then the 8-wave kernel over the last 256 rows in 128 x 256 tiles), timed together. Kernel times are medians of
+256 CUs, then the same kernel over the last 256 rows in 256 x 128 tiles), timed together. Kernel times are medians of
 HIP-event intervals on the launch stream.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
 rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
@@ -646,7 +646,7 @@ def main():
                    "weights": "bfp16ebs8 ~N(0,0.02)", "activations": "bf16 ~N(0,1)", "seed": 0},
         "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(up_tflops / PEAK_BF16_TFLOPS, 4), "traffic": UP_GEMM_TRAFFIC_BYTES,
-                     "kernel": "up GEMM 4352x3072x24576 + SwiGLU: gemm4w_kernel<1,8> rows 0..4095 + gemm8_kernel<1,4> rows 4096..4351",
+                     "kernel": "up GEMM 4352x3072x24576 + SwiGLU: gemm4w_kernel<1,8> rows 0..4095 + gemm4w_kernel<1,4> rows 4096..4351",
                      "us": round(r["ms_up"] * 1e3, 2)},
         "kernels": {
             # the kernel alone (graph replays); algorithmic bytes: bf16 read + packed written (the pass also writes

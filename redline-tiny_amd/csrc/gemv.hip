@@ -78,7 +78,7 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
     const int it = wave + kVWaves * idx;
 #pragma unroll
     for (int i = 0; i < 9; i++)
-      dw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], it * 8 * 9216, 0));
+      dw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], it * 8 * 9216, kLoadStream));
   };
   // iteration 0 goes straight to the wave's LDS buffer (lane l of load i lands at 1024 i + 16 l, the staged order)
   auto dma = [&](int idx) {
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
 #pragma unroll
     for (int i = 0; i < 9; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)&buf[wave][1024 * i], 16,
-                                               voff[i], it * 8 * 9216, 0, 0);
+                                               voff[i], it * 8 * 9216, 0, kLoadStream);
   };
 
   float part[M][16];

@@ -625,8 +625,8 @@ def main():
         sustain(args.sustain)
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by weight columns, "
-              "see DESIGN.md, but multi-GPU runs are not part of this build)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard by weight "
+              "columns across GPUs, which is not built)", file=sys.stderr)
         sys.exit(2)
     r = gpu_bench(args.steps, args.warmup, args.no_configs)
     ms_step = r["ms_step"]

@@ -1,7 +1,8 @@
 """CPU oracle for the bfp16 GEMM path: TEST INFRASTRUCTURE ONLY.
 
 Only the tests, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import this package, and
-only as the checker. The product (``redline-tiny_amd/``) never imports it and has no CPU fallback.
+only to check results against (or, in the baseline leg, to time the CPU path). The product (``redline-tiny_amd/``)
+never imports it and has no CPU fallback.
 
 Modules
   bfp16   the bfp16ebs8 format (encode / decode), the NPU stream layouts and the weight packer, restated in numpy

@@ -10,7 +10,7 @@ for p in (ROOT, os.path.join(ROOT, "redline-tiny_amd")):
 
 
 def pytest_configure(config):
-    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu on the GPU box")
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU; run with -m gpu on a machine that has one")
 
 
 @pytest.fixture(scope="session")

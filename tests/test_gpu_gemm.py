@@ -189,8 +189,8 @@ def test_grouped_non_bf16_a(dev, a_fmt):
 
 
 def test_config1_full_size_rows(dev):
-    """BASELINE config 1 at full size (A 4096x3072 ~N(0,1), W 3072x3072 ~N(0,0.02), seed 0): the GPU quantize pass
-    feeds the GEMM; 256 sampled rows are checked against the emulation, and the quantized A bit-exact."""
+    """The 4096 x 3072 x 3072 configuration at full size (A ~N(0,1), W 3072x3072 ~N(0,0.02), seed 0): the GPU
+    quantize pass feeds the GEMM; 256 sampled rows are checked against the emulation, and the quantized A bit-exact."""
     rng = np.random.default_rng(0)
     M = K = 4096
     K, N = 3072, 3072

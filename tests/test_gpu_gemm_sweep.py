@@ -119,3 +119,57 @@ def test_sweep(dev, M, K, N, ep, a_fmt, seed):
         vmax = blocks[np.arange(len(blocks)), np.abs(blocks).argmax(1)]
         corner = (vmax < 0) & (np.frexp(-vmax)[0] == 0.5)
         assert same[~corner].all()
+
+
+def _gemv_cases(n=16, seed=2027):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 9)), 64 * int(rng.integers(1, 97)), 128 * int(rng.integers(1, 65)),
+             "silu" if i % 2 == 0 else None, 300 + i) for i in range(n)]
+
+
+@pytest.mark.parametrize("M,K,N,act,seed", _gemv_cases())
+def test_gemv_sweep(dev, M, K, N, act, seed):
+    """The adaLN GEMV over M = 1..8, K to 6144 and N to 8192 (partial last iteration groups of K tiles, lanes past the
+    last K tile), against the emulation."""
+    rng = np.random.default_rng(seed)
+    x = F.bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    W = torch.from_numpy(G.linear_weight(rng, N, K)).cuda()
+    packed = ops.pack_weight(W)
+    got = ops.gemv(torch.from_numpy(x).cuda().bfloat16(), packed, N, act=act).float().cpu().numpy()
+    ref = G.gemv_ref(x, F.decode_b(packed.cpu().numpy(), K, N), act=act or "none")
+    assert G.rel_err(got, ref) <= 1e-2
+    d = np.abs(got.astype(np.float64) - ref)
+    assert (d <= 2 * np.abs(ref) * 2.0 ** -8 + 1e-5 * np.abs(ref).max()).mean() > 0.999
+
+
+def _group_cases(n=8, seed=2028):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        members = []
+        for j in range(int(rng.integers(2, 5))):
+            M = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 2500))]))
+            members.append((M, 64 * int(rng.integers(1, 25)), 128 * int(rng.integers(1, 17)),
+                            [None, "swiglu", "gelu_tanh", "bias"][int(rng.integers(0, 4))]))
+        out.append((members, 400 + i))
+    # the DiT block's shape of grouping: a 4096-row image stream and a 256-row text stream with separate weights
+    out.append(([(4096, 256, 2048, "swiglu"), (256, 256, 2048, "swiglu")], 450))
+    return out
+
+
+@pytest.mark.parametrize("members,seed", _group_cases())
+def test_grouped_sweep(dev, members, seed):
+    """Grouped launches of 2-4 members with different shapes and epilogues give the bits of the members' single
+    launches, whichever way the planner runs the group (one 8-wave launch, or each member as its own plan)."""
+    rng = np.random.default_rng(seed)
+    specs, refs = [], []
+    for M, K, N, ep in members:
+        a = torch.from_numpy(F.quantize_rows(G.activations(rng, M, K))).cuda().bfloat16()
+        b = ops.pack_weight(torch.from_numpy(G.linear_weight(rng, N, K)).cuda())
+        kw = {"act": ep} if ep in ("swiglu", "gelu_tanh") else {}
+        if ep in ("bias", "gelu_tanh"):
+            kw["bias"] = torch.from_numpy((rng.standard_normal(N) * 0.5).astype(np.float32)).cuda()
+        specs.append(ops.GemmSpec(a, b, N, K, **kw))
+        refs.append(ops.gemm(a, b, N, K, split=False, **kw))
+    for o, r in zip(ops.gemm_grouped(specs), refs):
+        assert torch.equal(o, r)

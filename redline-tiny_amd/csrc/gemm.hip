@@ -130,13 +130,14 @@ __device__ __forceinline__ int ep_slot(int c) { return c ^ ((c >> 4) & 15); }
 // re-quantize, all in fp32; returns the 8 bf16 as 4 words.
 __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int ocol, int nout, float (&v)[8]) {
   if (d.gate || d.res) {
-    const float* g = d.gate ? d.gate + (row < d.gate_split ? nout : 0) + ocol : nullptr;
+    f32x4 g4[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};  // NULL gate = 1
+    if (d.gate) __builtin_memcpy(g4, d.gate + (row < d.gate_split ? nout : 0) + ocol, 32);
     u32x4 r = {0u, 0u, 0u, 0u};
     if (d.res) r = *reinterpret_cast<const u32x4*>(d.res + (int64_t)row * d.ldr + ocol);
     const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const float gk = g ? g[k] : 1.0f;
+      const float gk = g4[k >> 2][k & 3];
       const float rk = __uint_as_float(k & 1 ? rw[k >> 1] & 0xFFFF0000u : rw[k >> 1] << 16);
       v[k] = rk + gk * v[k];
     }
@@ -158,13 +159,16 @@ __device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int oc
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int row = min(row0 + i, d.M - 1);
-      const float* g = d.gate ? d.gate + (row < d.gate_split ? nout : 0) + ocol : nullptr;
+      // the row's 8 gate values as two 16-byte loads under a wave-uniform test (NULL gate = 1): a per-value test of
+      // a per-lane pointer would branch around each load
+      f32x4 g4[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
+      if (d.gate) __builtin_memcpy(g4, d.gate + (row < d.gate_split ? nout : 0) + ocol, 32);
       u32x4 r = {0u, 0u, 0u, 0u};
       if (d.res) r = *reinterpret_cast<const u32x4*>(d.res + (int64_t)row * d.ldr + ocol);
       const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
       for (int k = 0; k < 8; k++) {
-        const float gk = g ? g[k] : 1.0f;
+        const float gk = g4[k >> 2][k & 3];
         const float rk = __uint_as_float(k & 1 ? rw[k >> 1] & 0xFFFF0000u : rw[k >> 1] << 16);
         v[i][k] = rk + gk * v[i][k];
       }
@@ -186,8 +190,10 @@ __device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int oc
 #pragma unroll
       for (int i = 0; i < 4; i++) o[i] = requantize8_fast(o[i], E[i]);
     } else {
+      // the integer encoder for all four blocks (it gives the fast path's bits wherever that applies), so neither
+      // side shares the other's per-block branches
 #pragma unroll
-      for (int i = 0; i < 4; i++) o[i] = requantize8(o[i]);
+      for (int i = 0; i < 4; i++) o[i] = quantize_bf16x8(o[i]);
     }
   }
 }
@@ -237,9 +243,10 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
       for (int k = 0; k < 8; k++) v[i][k] = a[k][i];
     u32x4 o[4];
     finish_rows4(d, row0, col, nout, v, o);
+    uint16_t* const c = d.C + (int64_t)row0 * d.ldc + col;  // the other rows at uniform strides of ldc
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      if (row0 + i < d.M) *reinterpret_cast<u32x4*>(d.C + (int64_t)(row0 + i) * d.ldc + col) = o[i];
+      if (row0 + i < d.M) *reinterpret_cast<u32x4*>(c + i * d.ldc) = o[i];
   }
 }
 

@@ -871,19 +871,40 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
 #pragma unroll
   for (int j = 0; j < 8; j++) bj[j] = d.bias ? d.bias[n0 + 16 * j + col_in] : 0.f;
   if (swiglu) {
-    // without a bias (the FFN up GEMMs) the two adds per output are left out of this transcendental-bound pass
+    // without a bias (the FFN up GEMMs) the two adds per output are left out of this transcendental-bound pass.
+    // Two fragments (8 outputs) go through each step of silu_f together, so that with one wave per SIMD the
+    // exp2 / reciprocal latencies of independent outputs overlap; per output the operations and their order are
+    // silu_f's.
     auto swiglu_pass = [&]<bool kBias>() {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int c = ep_slot(16 * g + col_in);
 #pragma unroll
-        for (int mf = 0; mf < MF; mf++) {
-          f32x4 v;
+        for (int mf = 0; mf < MF; mf += 2) {
+          const int nh = mf + 1 < MF ? 2 : 1;  // MF odd: the last step has one fragment
+          float x[8], u[8], e[8];
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            v[i] = kBias ? silu_f(acc[mf][g][i] + bj[g]) * (acc[mf][g + 4][i] + bj[g + 4])
-                         : silu_f(acc[mf][g][i]) * acc[mf][g + 4][i];
-          *reinterpret_cast<f32x4*>(ep + ((4 * MF * wave + 4 * mf + (lane >> 4)) * 64 + c) * 4) = v;
+          for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              x[4 * h + i] = h < nh ? (kBias ? acc[mf + h][g][i] + bj[g] : acc[mf + h][g][i]) : 0.f;
+              u[4 * h + i] = h < nh ? (kBias ? acc[mf + h][g + 4][i] + bj[g + 4] : acc[mf + h][g + 4][i]) : 0.f;
+            }
+#pragma unroll
+          for (int k = 0; k < 8; k++) e[k] = -1.4426950408889634f * x[k];
+#pragma unroll
+          for (int k = 0; k < 8; k++) e[k] = __builtin_amdgcn_exp2f(e[k]);
+#pragma unroll
+          for (int k = 0; k < 8; k++) e[k] = 1.0f + e[k];
+#pragma unroll
+          for (int k = 0; k < 8; k++) e[k] = __builtin_amdgcn_rcpf(e[k]);
+#pragma unroll
+          for (int k = 0; k < 8; k++) e[k] = (x[k] * e[k]) * u[k];
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+            if (h < nh)
+              *reinterpret_cast<f32x4*>(ep + ((4 * MF * wave + 4 * (mf + h) + (lane >> 4)) * 64 + c) * 4) =
+                  f32x4{e[4 * h], e[4 * h + 1], e[4 * h + 2], e[4 * h + 3]};
         }
       }
     };

@@ -69,13 +69,16 @@ __device__ __forceinline__ void unpack8(u32x4 v, float f[8]) {
 
 
 // Template NB = blocks of 8 per lane (D / 512 rounded up); lanes whose block lies past the row end hold zeros and
-// skip every access. The register budget per NB is the smallest that compiles without spills; for D = 3072 (NB 6)
-// it allows 5 waves per SIMD, so a launch of one wave per row for M = 4352 rows is resident in one round (at 4 waves
-// per SIMD a second, partial round would follow).
+// skip every access. Up to 8 blocks a row's first-pass loads are all in flight at once (in chunks of up to 6), which
+// needs more registers than one block at a time: the register budget per NB is the smallest that compiles without
+// spills. For D = 3072 (NB 6) it allows 4 waves per SIMD, so a launch of one wave per row for M = 4352 rows leaves a
+// short second round; that costs less than the per-block round trips of the 5-wave form (23.0 -> 22.0 us with a bf16
+// branch, 19.9 -> 18.6 us with a packed one, same bits).
 template <int NB>
-constexpr int ln_waves_per_simd() { return NB <= 5 ? 6 : NB <= 7 ? 5 : NB <= 13 ? 4 : 3; }
+constexpr int ln_waves_per_simd() { return NB <= 2 ? 6 : NB <= 4 ? 5 : NB <= 6 ? 4 : NB <= 8 ? 3 : NB <= 13 ? 4 : 3; }
 
-template <int NB>
+// BR: the branch's format for NB <= 8 (0 none, 1 bf16, 2 packed); above 8 blocks it is tested at run time (BR = -1)
+template <int NB, int BR>
 __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel(LnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t stage[];
   const int lane = threadIdx.x & 63;
@@ -91,47 +94,104 @@ __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel
     if (r >= a.M) break;
     const uint16_t* prm = a.params + (r < a.split_row ? 2 * (int64_t)D : 0);  // [g | sc] row
 
-    // x' = bf16(x + g * branch), kept as its bf16 bits (two per register: the row stays resident at 4 registers
-    // per block); sum for the mean
+    // x' = bf16(x + g * branch) of block j from its loaded words, kept as its bf16 bits (two per register: the row
+    // stays resident at 4 registers per block); sum for the mean. g * branch is exact in fp32: one rounding in the
+    // fma, then RNE to bf16; the mean's sum takes the bf16 pairs with one dot2 against (1, 1).
     u32x4 v[NB];
     float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
+    auto first = [&](int j, const u32x4& xw4, const u32x4& gw4, const float (&bf)[8]) {
       const int cb = lane + 64 * j;
-      v[j] = u32x4{0u, 0u, 0u, 0u};
-      if (cb < nbr) {
-        float xf[8], gf[8], bf[8];
-        unpack8(*reinterpret_cast<const u32x4*>(a.x + r * a.ldx + cb * 8), xf);
-        unpack8(*reinterpret_cast<const u32x4*>(prm + cb * 8), gf);
-        if (!a.br) {
+      float xf[8], gf[8];
+      unpack8(xw4, xf);
+      unpack8(gw4, gf);
+      uint32_t xw[4];
+      const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-          for (int e = 0; e < 8; e++) bf[e] = 0.f;
-        } else if (a.br_fmt == RL_BRANCH_BF16) {
-          unpack8(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.br) + r * a.ld_br + cb * 8), bf);
-        } else {
-          const int64_t blk = r * nbr + cb;
-          const Window w = load_window_safe(static_cast<const uint8_t*>(a.br), blk, a.M * nbr);
-          const uint32_t o = (uint32_t)(blk & 3);  // (9 * blk) % 4
-          const uint32_t lo = __builtin_amdgcn_alignbyte(w.w1, w.w0, o);
-          const uint32_t hi = __builtin_amdgcn_alignbyte(w.w2, w.w1, o);
-          const int sh = (int)(lo & 0xFFu) - 133;
-          const int32_t q[8] = {(int8_t)(lo >> 8), (int8_t)(lo >> 16), (int8_t)(lo >> 24), (int8_t)hi,
-                                (int8_t)(hi >> 8), (int8_t)(hi >> 16), (int8_t)(hi >> 24), (int8_t)(w.w2 >> (8 * o))};
+      for (int e = 0; e < 4; e++) {
+        const int i2 = 2 * e;
+        xw[e] = pack_bf16_rne(fmaf(gf[i2], bf[i2], xf[i2]), fmaf(gf[i2 + 1], bf[i2 + 1], xf[i2 + 1]));
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[e]), one, s, false);
+      }
+      v[j] = u32x4{xw[0], xw[1], xw[2], xw[3]};
+      if (a.x_out) *reinterpret_cast<u32x4*>(a.x_out + r * a.ld_xo + cb * 8) = v[j];
+    };
+    // a packed branch block from its 12-byte window (block blk starts at byte 9 blk): exact, as from_bfp16
+    auto branch_block = [&](int64_t blk, uint32_t w0, uint32_t w1, uint32_t w2, float (&bf)[8]) {
+      const uint32_t o = (uint32_t)(blk & 3);  // (9 * blk) % 4
+      const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, o);
+      const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, o);
+      const int sh = (int)(lo & 0xFFu) - 133;
+      const int32_t q[8] = {(int8_t)(lo >> 8), (int8_t)(lo >> 16), (int8_t)(lo >> 24), (int8_t)hi,
+                            (int8_t)(hi >> 8), (int8_t)(hi >> 16), (int8_t)(hi >> 24), (int8_t)(w2 >> (8 * o))};
 #pragma unroll
-          for (int e = 0; e < 8; e++) bf[e] = __builtin_amdgcn_ldexpf((float)q[e], sh);  // exact, as from_bfp16
+      for (int e = 0; e < 8; e++) bf[e] = __builtin_amdgcn_ldexpf((float)q[e], sh);
+    };
+    if constexpr (NB <= 8) {
+      // chunks of at most 6 blocks (4 for 7 or 8 blocks): every load of a chunk (x, the gate row and the branch;
+      // for the packed branch the block's 12-byte window in .x .y .z) is issued before any of them is used, so a
+      // row takes one or two memory round trips rather than one per block
+      constexpr int kMaxC = NB <= 6 ? 6 : 4, kNC = (NB + kMaxC - 1) / kMaxC, kC = (NB + kNC - 1) / kNC;
+#pragma unroll
+      for (int j0 = 0; j0 < NB; j0 += kC) {
+        u32x4 xr[kC], gr[kC], brw[kC];
+#pragma unroll
+        for (int c = 0; c < kC; c++) {
+          const int cb = lane + 64 * (j0 + c);
+          xr[c] = gr[c] = brw[c] = u32x4{0u, 0u, 0u, 0u};
+          if (j0 + c < NB && cb < nbr) {
+            xr[c] = *reinterpret_cast<const u32x4*>(a.x + r * a.ldx + cb * 8);
+            gr[c] = *reinterpret_cast<const u32x4*>(prm + cb * 8);
+            if constexpr (BR == 1) {
+              brw[c] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.br) + r * a.ld_br + cb * 8);
+            } else if constexpr (BR == 2) {
+              const Window w = load_window_safe(static_cast<const uint8_t*>(a.br), r * nbr + cb, a.M * nbr);
+              brw[c] = u32x4{w.w0, w.w1, w.w2, 0u};
+            }
+          }
         }
-        // g * branch is exact in fp32: one rounding in the fma, then RNE to bf16; the mean's sum takes the bf16 pairs
-        // with one dot2 against (1, 1)
-        uint32_t xw[4];
-        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int i = 2 * e;
-          xw[e] = pack_bf16_rne(fmaf(gf[i], bf[i], xf[i]), fmaf(gf[i + 1], bf[i + 1], xf[i + 1]));
-          s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[e]), one, s, false);
+        for (int c = 0; c < kC; c++) {
+          const int j = j0 + c;
+          if (j >= NB) break;
+          v[j] = u32x4{0u, 0u, 0u, 0u};
+          if (lane + 64 * j < nbr) {
+            float bf[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if constexpr (BR == 1) unpack8(brw[c], bf);
+            if constexpr (BR == 2) branch_block(r * nbr + lane + 64 * j, brw[c].x, brw[c].y, brw[c].z, bf);
+            first(j, xr[c], gr[c], bf);
+          }
         }
-        v[j] = u32x4{xw[0], xw[1], xw[2], xw[3]};
-        if (a.x_out) *reinterpret_cast<u32x4*>(a.x_out + r * a.ld_xo + cb * 8) = v[j];
+        // the next chunk's loads stay behind this chunk's math (registers)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // above 8 blocks: one block at a time, the branch's format tested at run time
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const int cb = lane + 64 * j;
+        v[j] = u32x4{0u, 0u, 0u, 0u};
+        if (cb < nbr) {
+          float bf[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          if (a.br && a.br_fmt == RL_BRANCH_BF16) {
+            unpack8(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.br) + r * a.ld_br + cb * 8), bf);
+          } else if (a.br) {
+            const Window w = load_window_safe(static_cast<const uint8_t*>(a.br), r * nbr + cb, a.M * nbr);
+            branch_block(r * nbr + cb, w.w0, w.w1, w.w2, bf);
+          }
+          first(j, *reinterpret_cast<const u32x4*>(a.x + r * a.ldx + cb * 8),
+                *reinterpret_cast<const u32x4*>(prm + cb * 8), bf);
+        }
+      }
+    }
+    // up to 8 blocks, the scale row's loads go out before the two reductions
+    constexpr bool kScaleEarly = NB <= 8;
+    u32x4 sr[kScaleEarly ? NB : 1];
+    if constexpr (kScaleEarly) {
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const int cb = lane + 64 * j;
+        sr[j] = u32x4{0u, 0u, 0u, 0u};
+        if (cb < nbr) sr[j] = *reinterpret_cast<const u32x4*>(prm + D + cb * 8);
       }
     }
     s = wave_sum(s);
@@ -158,7 +218,10 @@ __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel
       const int cb = lane + 64 * j;
       if (cb < nbr) {
         float sf[8], xf[8];
-        unpack8(*reinterpret_cast<const u32x4*>(prm + D + cb * 8), sf);
+        if constexpr (kScaleEarly)
+          unpack8(sr[j], sf);
+        else
+          unpack8(*reinterpret_cast<const u32x4*>(prm + D + cb * 8), sf);
         unpack8(v[j], xf);
         uint32_t u[8];
         int32_t q[8];
@@ -202,17 +265,30 @@ __global__ __launch_bounds__(kLnThreads, ln_waves_per_simd<NB>()) void ln_kernel
   }
 }
 
-template <int NB>
-static int launch_nb(const LnArgs& a, hipStream_t st) {
+template <int NB, int BR>
+static int launch_nb_br(const LnArgs& a, hipStream_t st) {
   const int64_t lds = a.a_packed ? (int64_t)a.rows_wg * (a.D / 8) * kBlockBytes : 0;
   if (lds > 65536) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ln_kernel<NB>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&ln_kernel<NB, BR>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return fail(RL_ERR_DEVICE, "hipFuncSetAttribute: %s", hipGetErrorString(e));
   }
   const dim3 grid((unsigned)((a.M + a.rows_wg - 1) / a.rows_wg));
-  hipLaunchKernelGGL(ln_kernel<NB>, grid, dim3(kLnThreads), (unsigned)lds, st, a);
+  hipLaunchKernelGGL((ln_kernel<NB, BR>), grid, dim3(kLnThreads), (unsigned)lds, st, a);
   return launch_status("rl_ln_modulate");
+}
+
+// the branch's format is a template parameter, so that the first pass is straight-line code whose loads all issue
+// before the first use
+template <int NB>
+static int launch_nb(const LnArgs& a, hipStream_t st) {
+  if constexpr (NB > 8) {
+    return launch_nb_br<NB, -1>(a, st);
+  } else {
+    if (!a.br) return launch_nb_br<NB, 0>(a, st);
+    if (a.br_fmt == RL_BRANCH_BF16) return launch_nb_br<NB, 1>(a, st);
+    return launch_nb_br<NB, 2>(a, st);
+  }
 }
 
 template <int NB>

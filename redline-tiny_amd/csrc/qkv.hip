@@ -97,19 +97,29 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
     float wf[8];
     unpack8f(*reinterpret_cast<const u32x4*>((part ? a.wk : a.wq) + bc * 8), wf);
     uint16_t* nat = NATIVE ? (part ? a.k : a.q) : nullptr;
+    // every pass's loads (the token's 8 values, its cos and sin) are issued before the first use: the encoder's
+    // rarely taken integer path is a branch that later loads are not hoisted over
+    u32x4 xr[4];
+    uint2 cr4[4], sr4[4];
+#pragma unroll
+    for (int pass = 0; pass < 4; pass++) {
+      const int64_t row = row0 + pass * 16 + rr;
+      xr[pass] = *reinterpret_cast<const u32x4*>(a.C + row * a.ldc + col0 + bc * 8);
+      cr4[pass] = *reinterpret_cast<const uint2*>(a.cos + row * 64 + bc * 4);
+      sr4[pass] = *reinterpret_cast<const uint2*>(a.sin + row * 64 + bc * 4);
+    }
 #pragma unroll
     for (int pass = 0; pass < 4; pass++) {
       const int r = pass * 16 + rr;
       const int64_t row = row0 + r;
       float xf[8];
-      unpack8f(*reinterpret_cast<const u32x4*>(a.C + row * a.ldc + col0 + bc * 8), xf);
+      unpack8f(xr[pass], xf);
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; e++) ss = fmaf(xf[e], xf[e], ss);
       ss = row16_sum(ss);  // the token's 16 lanes
       const float inv = __builtin_amdgcn_rsqf(ss / (float)kHeadDim + 1e-6f);
-      const uint2 cr = *reinterpret_cast<const uint2*>(a.cos + row * 64 + bc * 4);
-      const uint2 sr = *reinterpret_cast<const uint2*>(a.sin + row * 64 + bc * 4);
+      const uint2 cr = cr4[pass], sr = sr4[pass];
       const float c4[4] = {__uint_as_float(cr.x << 16), __uint_as_float(cr.x & 0xFFFF0000u),
                            __uint_as_float(cr.y << 16), __uint_as_float(cr.y & 0xFFFF0000u)};
       const float s4[4] = {__uint_as_float(sr.x << 16), __uint_as_float(sr.x & 0xFFFF0000u),
@@ -132,6 +142,14 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
   } else {
     // V: thread = (dim d, 8-token block kb), reading its 8 tokens of one dim (consecutive lanes read consecutive
     // dims: 128 contiguous bytes of a row per load); b_layout(V, 64, 128): 16-dim band, token block, 8-dim half, dim
+    // all four items' loads first, as for Q and K
+    uint16_t vr[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int item = tid + kQkvThreads * i, d = item & 127, kb = item >> 7;
+#pragma unroll
+      for (int e = 0; e < 8; e++) vr[i][e] = a.C[(row0 + kb * 8 + e) * a.ldc + col0 + d];
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int item = tid + kQkvThreads * i, d = item & 127, kb = item >> 7;
@@ -139,7 +157,7 @@ __global__ __launch_bounds__(kQkvThreads) void qkv_post_kernel(QkvArgs a) {
       int32_t q[8];
       u32x4 bw;
 #pragma unroll
-      for (int e = 0; e < 8; e++) u[e] = (uint32_t)a.C[(row0 + kb * 8 + e) * a.ldc + col0 + d] << 16;
+      for (int e = 0; e < 8; e++) u[e] = (uint32_t)vr[i][e] << 16;
       const uint32_t E = encode_block(u, q, bw);
       if (NATIVE && a.v)  // V^T: the block's 8 tokens are contiguous in row d
         *reinterpret_cast<u32x4*>(a.v + ((int64_t)h * kHeadDim + d) * a.M + row0 + kb * 8) = bw;

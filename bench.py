@@ -174,6 +174,15 @@ def gpu_bench(steps, warmup, no_configs=False):
 
     us_q_alone = graph_us(quantize_rot, 8, 40, 5)
     assert torch.equal(qq[0], xq), "the quantize pass in graph replays differs from the step's"
+
+    # the same pass with the packed output only (to_bfp16 alone: 2 bytes read, 9/8 written per value)
+    def quantize_packed_rot(i):
+        j = i % 4
+        L.check(L.lib().rl_bfp16_quantize(ctypes.c_void_p(qx[j].data_ptr()), L.RL_DTYPE_BF16, M, K, K,
+                                          L.RL_ORDER_ROWBLOCK, ctypes.c_void_p(qp[j].data_ptr()), None, stream()))
+
+    us_q_packed = graph_us(quantize_packed_rot, 8, 40, 5)
+    assert torch.equal(qp[0], xp), "the packed-only quantize pass differs from the step's packed bytes"
     del qx, qp, qq
 
     # GEMV: M = 1 adaLN modulation, weights rotated over 6 copies (382 MB > 256 MB MALL)
@@ -213,7 +222,8 @@ def gpu_bench(steps, warmup, no_configs=False):
     return {
         "host": host, "p_up": inp["up"].cpu().numpy(), "p_down": inp["down"].cpu().numpy(),
         "wall_s": wall, "ms_step": ms_step, "ms_step_eager": ms_step_eager,
-        "ms_q": ms_q, "us_q_alone": us_q_alone, "ms_up": ms_up, "ms_down": ms_down, "us_gemv": us_gemv,
+        "ms_q": ms_q, "us_q_alone": us_q_alone, "us_q_packed": us_q_packed, "ms_up": ms_up, "ms_down": ms_down,
+        "us_gemv": us_gemv,
         "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
         "v9a": v9a,
         "ln": ln_bench(dev),
@@ -653,6 +663,9 @@ def main():
             # the decoded bf16 copy the GEMM reads, not counted)
             "quantize_us": round(r["us_q_alone"], 2),
             "quantize_gbps": round(M * K * (2 + 9 / 8) / (r["us_q_alone"] * 1e-6) / 1e9, 1),
+            "quantize_packed_only_us": round(r["us_q_packed"], 2),
+            "quantize_packed_only_frac_hbm": round(M * K * (2 + 9 / 8) / (r["us_q_packed"] * 1e-6) / 1e9
+                                                   / PEAK_HBM_GBPS, 4),
             "quantize_in_step_us": round(r["ms_q"] * 1e3, 2),
             "up_us": round(r["ms_up"] * 1e3, 2), "up_tflops": round(up_tflops, 2),
             "down_us": round(r["ms_down"] * 1e3, 2),

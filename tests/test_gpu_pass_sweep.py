@@ -69,6 +69,12 @@ def _ln_cases(n=12, seed=2030):
         M = 128 * int(rng.integers(1, 6)) if a_order == "a_layout" else int(rng.integers(1, 600))
         out.append((M, D, [None, "bf16", "packed"][i % 3], "rms" if i % 2 else "layer", a_order,
                     int(rng.integers(0, M + 1)), 600 + i))
+    # every form of the kernel's first pass: one chunk (2 and 6 blocks per lane), two chunks (7 and 8), one block at
+    # a time (9 and more), with the three branch formats among them; split rows at 0, inside and at M
+    out += [(301, 1024, "packed", "layer", "rowblock", 100, 620), (96, 3072, None, "rms", "rowblock", 0, 621),
+            (257, 3584, "packed", "layer", "rowblock", 257, 622), (128, 3584, "bf16", "rms", "a_layout", 64, 623),
+            (130, 4096, None, "layer", "rowblock", 7, 624), (77, 4096, "bf16", "layer", "rowblock", 40, 625),
+            (33, 4608, "packed", "rms", "rowblock", 1, 626), (2, 8192, "bf16", "layer", "rowblock", 1, 627)]
     return out
 
 

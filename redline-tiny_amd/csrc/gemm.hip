@@ -49,7 +49,7 @@ struct GemmDesc {
   const uint16_t* res;
   int64_t ldr;
   int32_t tiles_m, tiles_n, tile_start;
-  int32_t ksplit;  // K pieces (8-wave kernel): 1 = whole K; > 1 = each piece writes fp32 partials to `part`
+  int32_t ksplit;  // K pieces: 1 = whole K; > 1 = each piece writes fp32 partials to `part`
   float* part;     // [ksplit][M][N] fp32 partial sums of the pieces, summed by gemm_reduce_kernel
 };
 
@@ -683,6 +683,27 @@ constexpr int kW4Threads = 256;
 constexpr int kW4BStage = 1024 * 16;  // decoded blocks of one 64 x 128 b_layout tile
 constexpr int kW4GroupM = 2;           // M-tiles per group in an XCD's tile range (x 16 N-tiles: 32 CUs)
 
+// The K-piece store of the 4-wave kernel: the LDS tile holds raw fp32 sums of `nquads` row quads x 128 computed columns
+// (staged column c is column c0 + c); each thread stores blocks of 4 rows x 8 columns to plane `piece` of d.part.
+__device__ __forceinline__ void ep4_partial(const GemmDesc& d, const float* ep, int r0, int c0, int nquads, int piece,
+                                            int tid) {
+  for (int it = tid; it < nquads * 16; it += kW4Threads) {
+    const int q = it >> 4, cb = it & 15;
+    const int col = c0 + 8 * cb;
+    f32x4 a[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * 128 + ep_slot(8 * cb + k)) * 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = r0 + 4 * q + i;
+      if (row >= d.M) break;
+      float* dst = d.part + ((int64_t)piece * d.M + row) * d.N + col;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{a[0][i], a[1][i], a[2][i], a[3][i]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{a[4][i], a[5][i], a[6][i], a[7][i]};
+    }
+  }
+}
+
 template <int G, int MF>
 __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G> args) {
   static_assert(MF >= 4 && MF <= 8, "four decode octets per phase, 8 x 8 accumulators at most");
@@ -700,7 +721,14 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
       if (pid >= args.d[i].tile_start) di = i;
   }
   const GemmDesc& d = args.d[di];
-  const int local = pid - d.tile_start;
+  int local = pid - d.tile_start;
+  // K pieces: piece p covers K steps [p KT / ksplit, (p + 1) KT / ksplit) of every tile; the workgroups of a piece
+  // are tiles_m * tiles_n apart
+  int piece = 0;
+  if (d.ksplit > 1) {
+    piece = local / (d.tiles_m * d.tiles_n);
+    local -= piece * d.tiles_m * d.tiles_n;
+  }
   const int group = local / (kW4GroupM * d.tiles_n);
   const int first_m = group * kW4GroupM;
   const int gm = min(d.tiles_m - first_m, kW4GroupM);
@@ -710,7 +738,9 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS and row offsets stay scalar
-  const int KT = d.K / BK;
+  const int KTt = d.K / BK;                    // K steps of the whole GEMM
+  const int kb = piece * KTt / d.ksplit;        // this piece's first K step
+  const int KT = (piece + 1) * KTt / d.ksplit - kb;
   const bool swiglu = d.act == RL_ACT_SWIGLU;
 
   const __amdgpu_buffer_rsrc_t brs =
@@ -721,7 +751,7 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
   // B decode: thread t decodes blocks 4t .. 4t + 3 of the step's b_layout tile, a 36-byte dword-aligned run, read
   // with three loads (bytes 0..15, 16..31, 32..35). The four blocks are lanes 4 (t % 16) + J of fragment t / 16 =
   // 2 g + h (column group g, K half h).
-  const uint32_t vb = (uint32_t)((int64_t)(n0 >> 7) * KT * kTileBytes + 36 * tid);
+  const uint32_t vb = (uint32_t)(((int64_t)(n0 >> 7) * KTt + kb) * kTileBytes + 36 * tid);
   uint32_t st_off[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) st_off[j] = (tid >> 4) * 1024 + 16 * frag_pos(4 * (tid & 15) + j);
@@ -753,8 +783,8 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
   // buffer range check covers the vector offset), the K step in the scalar offset. Rows past M lie past the end of
   // the buffer resource and read zeros.
   const int ar0 = 8 * kDma * wave + (lane >> 3);
-  const uint32_t va_e = (uint32_t)(((int64_t)(m0 + ar0) * d.lda + ((lane & 7) ^ a_swz(ar0)) * 8) * 2);
-  const uint32_t va_o = (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + ((lane & 7) ^ a_swz(ar0 + 8)) * 8) * 2);
+  const uint32_t va_e = (uint32_t)(((int64_t)(m0 + ar0) * d.lda + ((lane & 7) ^ a_swz(ar0)) * 8 + kb * BK) * 2);
+  const uint32_t va_o = (uint32_t)(((int64_t)(m0 + ar0 + 8) * d.lda + ((lane & 7) ^ a_swz(ar0 + 8)) * 8 + kb * BK) * 2);
   const uint32_t row16 = (uint32_t)(16 * d.lda * 2);
   auto dma_a = [&](int stage, int k, int i) {
     uint8_t* dst = lds + stage * kAS + 8 * (kDma * wave + i) * (BK * 2);
@@ -870,7 +900,7 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
   float bj[8];
 #pragma unroll
   for (int j = 0; j < 8; j++) bj[j] = d.bias ? d.bias[n0 + 16 * j + col_in] : 0.f;
-  if (swiglu) {
+  if (swiglu && d.ksplit == 1) {
     // without a bias (the FFN up GEMMs) the two adds per output are left out of this transcendental-bound pass.
     // Two fragments (8 outputs) go through each step of silu_f together, so that with one wave per SIMD the
     // exp2 / reciprocal latencies of independent outputs overlap; per output the operations and their order are
@@ -932,11 +962,14 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
         }
       }
     };
-    const bool gelu = d.act == RL_ACT_GELU_TANH;
+    // a K piece stages its raw fp32 sums (no bias, activation or SwiGLU product) and stores them to its partial plane
+    const bool gelu = d.act == RL_ACT_GELU_TANH, part = d.ksplit > 1;
 #pragma unroll
     for (int P = 0; P < 2; P++) {
       if ((wave >> 1) == P) {
-        if (gelu)
+        if (part)
+          stage_pass.template operator()<false, false>();
+        else if (gelu)
           stage_pass.template operator()<true, true>();
         else if (d.bias)
           stage_pass.template operator()<true, false>();
@@ -944,7 +977,10 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
           stage_pass.template operator()<false, false>();
       }
       __syncthreads();
-      ep8_finish<128, kW4Threads>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
+      if (part)
+        ep4_partial(d, ep, m0 + TM / 2 * P, n0, TM / 8, piece, tid);
+      else
+        ep8_finish<128, kW4Threads>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
       __syncthreads();
     }
   }
@@ -1104,6 +1140,7 @@ static PlanG plan_gemm(int64_t M, int64_t N, int cus, int act, double* cost = nu
 // ksplit fp32 planes of M x N and writes the output: kReduceUs + bytes / kReduceBw. A split, with every piece in one
 // round, is taken when the model puts it under 3/4 of the best whole-K launch.
 constexpr double kStepUs = 0.18, kTileUs = 3.0, kReduceUs = 2.0, kReduceBw = 4.0e6;  // kReduceBw: bytes per us
+constexpr double kStep4Us = 0.157;
 constexpr int kMaxSplit = 16, kMinPieceSteps = 8;
 constexpr int64_t kMaxSplitBytes = int64_t(1) << 30;
 
@@ -1111,13 +1148,17 @@ struct SplitPlan {
   int mf;            // fragments per wave
   int ks;            // K pieces; 1 = no split
   int64_t ws_bytes;  // fp32 partial planes: ks * M * N * 4
+  bool w4;           // pieces on the 4-wave kernel (64 MF x 128 tiles) rather than the 8-wave one (32 MF x 256)
 };
 
 static SplitPlan plan_split(int64_t M, int64_t N, int64_t K, int cus) {
-  SplitPlan best{8, 1, 0};
+  SplitPlan best{8, 1, 0, false};
   if (cus <= 0) return best;
   const int64_t KT = K / BK;
   auto tile_us = [](int mf, int64_t steps) { return (double)steps * (mf + 1) * kStepUs + kTileUs; };
+  // a 4-wave tile (the same MFMA work per MF) costs (MF + 0.9) kStep4Us per K step: 1.4 us per step at MF = 8 on
+  // the FFN up GEMM, against 1.6 for the 8-wave tile
+  auto tile4_us = [](int mf, int64_t steps) { return (double)steps * (mf + 0.9) * kStep4Us + kTileUs; };
   double whole = 1e300;
   for (int mf : kMfChoices) {
     const int64_t t = tiles8(M, N, mf);
@@ -1125,15 +1166,18 @@ static SplitPlan plan_split(int64_t M, int64_t N, int64_t K, int cus) {
     if (c < whole) whole = c;
   }
   double bc = 0.75 * whole;
-  for (int mf : kMfChoices) {
-    const int64_t t = tiles8(M, N, mf);
-    for (int ks = 2; ks <= kMaxSplit && t * ks <= cus && KT / ks >= kMinPieceSteps; ks++) {
-      const int64_t bytes = (int64_t)ks * M * N * 4;
-      if (bytes > kMaxSplitBytes) break;
-      const double c = tile_us(mf, (KT + ks - 1) / ks) + kReduceUs + (double)(bytes + M * N) / kReduceBw;
-      if (c < bc) { bc = c; best = SplitPlan{mf, ks, bytes}; }
+  for (int w4 = 0; w4 < 2; w4++)
+    for (int mf : kMfChoices) {
+      const int64_t t = w4 ? tiles4(M, N, mf) : tiles8(M, N, mf);
+      for (int ks = 2; ks <= kMaxSplit && t * ks <= cus && KT / ks >= kMinPieceSteps; ks++) {
+        const int64_t bytes = (int64_t)ks * M * N * 4;
+        if (bytes > kMaxSplitBytes) break;
+        const int64_t steps = (KT + ks - 1) / ks;
+        const double c =
+            (w4 ? tile4_us(mf, steps) : tile_us(mf, steps)) + kReduceUs + (double)(bytes + M * N) / kReduceBw;
+        if (c < bc) { bc = c; best = SplitPlan{mf, ks, bytes, w4 != 0}; }
+      }
     }
-  }
   return best;
 }
 
@@ -1163,7 +1207,7 @@ static int launch8(const GemmArgs<G>& args, int total_tiles, int mf, void* strea
   return launch_status("rl_bfp16_gemm");
 }
 
-// Tiles of the 4-wave kernel: 64 mf rows x 128 columns (one b_layout N-tile); whole K only.
+// Tiles of the 4-wave kernel: 64 mf rows x 128 columns (one b_layout N-tile), times the K pieces.
 template <int G>
 static void set_tiles4w(GemmArgs<G>& args, int mf, int& total) {
   total = 0;
@@ -1172,7 +1216,7 @@ static void set_tiles4w(GemmArgs<G>& args, int mf, int& total) {
     g.tiles_m = (int32_t)((g.M + 64 * mf - 1) / (64 * mf));
     g.tiles_n = (int32_t)(g.N / 128);
     g.tile_start = total;
-    total += g.tiles_m * g.tiles_n;
+    total += g.tiles_m * g.tiles_n * g.ksplit;
   }
   for (int i = args.n; i < G; i++) args.d[i] = args.d[args.n - 1];
 }
@@ -1327,8 +1371,13 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
                     (long long)workspace_bytes, (long long)sp.ws_bytes);
       args.d[0].ksplit = sp.ks;
       args.d[0].part = static_cast<float*>(workspace);
-      set_tiles8(args, sp.mf, total);
-      if ((s = launch8<1>(args, total, sp.mf, stream))) return s;
+      if (sp.w4) {
+        set_tiles4w(args, sp.mf, total);
+        if ((s = launch4w<1>(args, total, sp.mf, stream))) return s;
+      } else {
+        set_tiles8(args, sp.mf, total);
+        if ((s = launch8<1>(args, total, sp.mf, stream))) return s;
+      }
       const int64_t nblocks = M * ((ep && ep->act == RL_ACT_SWIGLU) ? N / 2 : N) / 8;
       hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0,
                          static_cast<hipStream_t>(stream), args.d[0]);

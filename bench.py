@@ -36,7 +36,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (vendor figure)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # HBM bytes per up-GEMM call (its two launches) from rocprofv3 FETCH_SIZE (x2) and WRITE_SIZE (x1), the factors that make a 256 MB
 # device-to-device copy read and write 256 MB (profiles/gemm_dit_ffn_counters.md); re-measured when the kernel changes
-UP_GEMM_TRAFFIC_BYTES = 846812701
+UP_GEMM_TRAFFIC_BYTES = 846841373
 M, K, FF = 4352, 3072, 12288
 GEMV_K, GEMV_N = 3072, 18432
 

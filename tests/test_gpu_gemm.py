@@ -244,10 +244,12 @@ def _split_case(M, K, N, seed, act=None):
     return rng, F.quantize_rows(A), packed, F.decode_b(packed, K, N)
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 8192, 512), (100, 4096, 384), (512, 3072, 3072)])
+@pytest.mark.parametrize("M,K,N", [(256, 8192, 512), (100, 4096, 384), (512, 3072, 3072), (16, 8192, 3072)])
 def test_k_split_plain(dev, M, K, N):
     """Small-M, deep-K shapes split K into pieces (fp32 partials in a workspace, summed in piece order): against the
-    emulation, and against the whole-K kernel to within the fp32 summation difference."""
+    emulation, and against the whole-K kernel to within the fp32 summation difference. The first three split on the
+    4-wave kernel (64-row fragments, 128 columns); 16 x 3072 x 8192 splits 16 ways on the 8-wave kernel (a 128-row
+    tile holding 16 rows, 256 columns)."""
     assert ops.gemm_workspace_bytes(M, N, K) > 0
     rng, Aq, packed, Bq = _split_case(M, K, N, M + K)
     a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)

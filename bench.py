@@ -226,6 +226,7 @@ def gpu_bench(steps, warmup, no_configs=False):
         "us_gemv": us_gemv,
         "gemv_gbps": gemv_bytes / (us_gemv * 1e-6) / 1e9, "gemv_bytes": gemv_bytes,
         "v9a": v9a,
+        "v9_ops": v9_oplist_bench(dev),
         "ln": ln_bench(dev),
         "qkv": qkv_bench(dev),
         "attn": attn_bench(dev),
@@ -426,6 +427,76 @@ def configs_bench(dev, per_graph=10, reps=3):
             ops.gemm_grouped(specs)
 
     out["cfg5"] = line(graph_us(cfg5, 5, per_graph, reps), 2.0 * 4352 * K * (9216 + K + 2 * 12288 + 12288))
+    return out
+
+
+def v9_oplist_bench(dev, per_graph=5, reps=3):
+    """The DiT block's GEMMs in the order CachedStep.blocks issues them (redline/forward.py:240-254: qkv, o,
+    up_swiglu, down), through the NPU.run mirror on the reference's own buffers: A as the V9 a_layout stream, C as the
+    ATB bfp16 stream, H in the down GEMM's A layout (each GEMM's epilogue writes the packed blocks itself; a V9 A is
+    staged as bf16 in a workspace first). Beside them: the same GEMMs on the native operands (bf16 A and C), and
+    bf16 A with the V9 C (the cost of the packed output alone). Hidden 3072, FF 12288, M = 4608: the 4352 tokens of
+    the benchmark padded to a multiple of 512, as the reference's ATB artifacts need (its cfg2 note). HIP-graph
+    replays; every V9 output is checked against the quantize pass over the native output."""
+    import torch
+
+    from rlbfp import forward as FW
+    from rlbfp import ops
+
+    Mp, H, Fh = 4608, K, FF
+    g = torch.Generator(device=dev).manual_seed(21)
+    w = {"qkv": ops.pack_weight(torch.randn((3 * H, H), generator=g, device=dev) * 0.02),
+         "o": ops.pack_weight(torch.randn((H, H), generator=g, device=dev) * 0.02),
+         "up": ops.pack_weight(ops.interleave_up(torch.randn((Fh, H), generator=g, device=dev) * 0.02,
+                                                 torch.randn((Fh, H), generator=g, device=dev) * 0.02).contiguous()),
+         "down": ops.pack_weight(torch.randn((H, Fh), generator=g, device=dev) * 0.02)}
+    # the V9 A streams encode the raw activations; the native bf16 A holds their values
+    x_raw = torch.randn((Mp, H), generator=g, device=dev).to(torch.bfloat16)
+    o_raw = torch.randn((Mp, H), generator=g, device=dev).to(torch.bfloat16)
+    x, o = ops.quantize(x_raw, deq=True)[1], ops.quantize(o_raw, deq=True)[1]
+    a9, o9 = ops.quantize(x_raw, order="a_layout")[0], ops.quantize(o_raw, order="a_layout")[0]
+    npu = FW.NPU(kn={"qkv": (H, 3 * H), "o": (H, H), "up": (H, 2 * Fh), "down": (Fh, H)})
+    c_qkv9, c9, h9 = FW.v9(Mp * 3 * H, dev), FW.v9(Mp * H, dev), FW.v9(Mp * Fh, dev)
+    c_qkv, c, h = (torch.empty((Mp, n), dtype=torch.bfloat16, device=dev) for n in (3 * H, H, Fh))
+    h_a9 = torch.empty_like(h9)
+    # (op, V9 call, native call, V9 C from the native bf16 A, check: V9 output against the native one)
+    ops_ = {
+        "qkv": (lambda: npu._gemm("qkv", "atb3d2-qkv", a9, w["qkv"], c_qkv9),
+                lambda: ops.gemm(x, w["qkv"], 3 * H, H, out=c_qkv),
+                lambda: ops.gemm(x, w["qkv"], 3 * H, H, packed_out=c_qkv9),
+                lambda: torch.equal(c_qkv9, ops.quantize(c_qkv, order="c_atb")[0])),
+        "o": (lambda: npu._gemm("o", "atb3d2-4096", o9, w["o"], c9),
+              lambda: ops.gemm(o, w["o"], H, H, out=c),
+              lambda: ops.gemm(o, w["o"], H, H, packed_out=c9),
+              lambda: torch.equal(c9, ops.quantize(c, order="c_atb")[0])),
+        # H as the reference pushes it: the bfp16 blocks of the bf16 SwiGLU output; the native H (re-quantized in
+        # the epilogue) holds their values
+        "up_swiglu": (lambda: npu._gemm("up_swiglu", "atb3sw2-m4608", a9, w["up"], h9),
+                      lambda: ops.gemm(x, w["up"], 2 * Fh, H, act="swiglu", quantize_out=True, out=h),
+                      lambda: ops.gemm(x, w["up"], 2 * Fh, H, act="swiglu", packed_out=h9, packed_order="a_layout"),
+                      lambda: torch.equal(ops.dequantize(h9, Mp, Fh, order="a_layout", dtype=torch.bfloat16), h)),
+        "down": (lambda: npu._gemm("down", "atb3d2-down", h_a9, w["down"], c9),
+                 lambda: ops.gemm(h, w["down"], H, Fh, out=c),
+                 lambda: ops.gemm(h, w["down"], H, Fh, packed_out=c9),
+                 lambda: torch.equal(c9, ops.quantize(c, order="c_atb")[0])),
+    }
+    out = {"M": Mp, "hidden": H, "ff": Fh}
+    tot = {"v9": 0.0, "native": 0.0, "v9c_bf16a": 0.0}
+    for name, (v9call, native, v9c, check) in ops_.items():
+        if name == "down":
+            h_a9.copy_(h9)  # the down GEMM's V9 A: H as up_swiglu pushed it
+        us_n = graph_us(lambda i: native(), 2, per_graph, reps)
+        us_c = graph_us(lambda i: v9c(), 2, per_graph, reps)
+        assert check(), f"{name}: the V9 C from bf16 A differs from the quantize pass over the bf16 C"
+        us_v = graph_us(lambda i: v9call(), 2, per_graph, reps)
+        assert check(), f"{name}: the V9 op differs from the quantize pass over the native output"
+        out[name] = {"v9_us": round(us_v, 2), "native_us": round(us_n, 2), "v9c_bf16a_us": round(us_c, 2),
+                     "v9c_vs_bf16c": round(us_c / us_n, 4)}
+        tot["v9"] += us_v
+        tot["native"] += us_n
+        tot["v9c_bf16a"] += us_c
+    out["total"] = {k + "_us": round(v, 2) for k, v in tot.items()}
+    out["total"]["v9_vs_native"] = round(tot["v9"] / tot["native"], 4)
     return out
 
 
@@ -678,6 +749,7 @@ def main():
         "gemv": {"shape": [1, GEMV_K, GEMV_N], "us": round(r["us_gemv"], 2), "gbps": round(r["gemv_gbps"], 1),
                  "frac_hbm": round(r["gemv_gbps"] / PEAK_HBM_GBPS, 4), "bytes": int(r["gemv_bytes"]),
                  "copies": 6},
+        "v9_oplist": r["v9_ops"],
         "ln_modulate": r["ln"],
         "qkv_post": r["qkv"],
         "attention": r["attn"],

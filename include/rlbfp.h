@@ -7,7 +7,9 @@
  * Conventions for every entry point:
  *   - pointers are device pointers (HIP global memory) unless stated; sizes are int64 element counts;
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); work is enqueued, never synchronised;
- *   - outputs are caller-allocated; no entry point allocates device memory;
+ *   - outputs are caller-allocated. No entry point allocates device memory, with one exception: rl_bfp16_gemm and
+ *     rl_bfp16_gemm_grouped given an A in a format other than RL_A_BF16 stage it as bf16 in a stream-ordered
+ *     allocation (hipMallocAsync / hipFreeAsync on the call's stream; refused under graph capture);
  *   - the return value is RL_OK (0) or an RL_ERR_* code; rl_last_error() gives a message for the calling thread.
  * The reference's interfaces are Python (numpy host code and NPU artifacts run through XRT); each declaration cites
  * the reference function it replaces.
@@ -64,7 +66,7 @@ int rl_bfp16_dequantize(const uint8_t *packed, int32_t order, int64_t rows, int6
  * fp32 accumulation on bf16 MFMA, bf16 output. M >= 1, N % 128 == 0, K % 64 == 0.                                  */
 enum {
   RL_A_BF16 = 0,          /* bf16 row major, used as is (already bfp16 values, e.g. rl_bfp16_quantize's deq)  */
-  RL_A_BF16_QUANTIZE = 1, /* bf16 row major, quantized to bfp16 along K while it is loaded                     */
+  RL_A_BF16_QUANTIZE = 1, /* bf16 row major, quantized to bfp16 along K by a staging pass before the product    */
   RL_A_PACKED_ROWBLOCK = 2, /* packed, RL_ORDER_ROWBLOCK of (M, K); lda ignored                                   */
   RL_A_PACKED_A_LAYOUT = 3  /* packed, RL_ORDER_A_LAYOUT of (M, K) (the NPU's A operand); M%128 == 0; lda ignored */
 };
@@ -75,14 +77,28 @@ enum {
                            out[:, 64t+u] = silu(v[:, 128t+u]) * v[:, 128t+64+u] (kernels/atb3/mm_bfp_swiglu.cc)  */
 };
 enum {
-  RL_EP_QUANTIZE_OUT = 1 /* after the bf16 rounding, re-quantize each 8-column block of the output to bfp16 (the
-                            stored bf16 values are then exact bfp16 values, ready as the next GEMM's RL_A_BF16)    */
+  RL_EP_QUANTIZE_OUT = 1, /* after the bf16 rounding, re-quantize each 8-column block of the output to bfp16 (the
+                             stored bf16 values are then exact bfp16 values, ready as the next GEMM's RL_A_BF16)   */
+  RL_EP_WHOLE_K = 2       /* rl_bfp16_gemm_ws: never split K, whatever the workspace; the workspace then needs only
+                             the staged bf16 copy of a non-bf16 A (M * K * 2 bytes rounded up to 256), or nothing */
+};
+
+/* Layout of the bf16 C. */
+enum {
+  RL_C_ROWMAJOR = 0, /* (M, Nout) row major, leading dimension ldc */
+  RL_C_ATB = 1       /* flat, the c_layout_atb(., 128, 128) element order (npu_layouts.py:42-47), i.e. the C16
+                        artifacts' output (kernels/vlm/mm_bfp_c16.cc:1-2); M % 512 == 0, Nout % 1024 == 0; ldc ignored */
 };
 
 /* Fused epilogue, applied in fp32 in this order: v = acc + bias[n]; v = act(v); v = residual[m][n] + g[n] * v with
  * g = gate row 1 for rows < gate_split_row else gate row 0 (gate NULL = 1); out = bf16(v) (RNE); optional
  * re-quantize. The gate/residual step is the adaLN "x' = x + g * branch" (redline/run_ln.py:65-67, rows_param
- * :82-86; kernels/glue/ln_mod.cc:92-143) fused into the producing GEMM. n indexes output columns. */
+ * :82-86; kernels/glue/ln_mod.cc:92-143) fused into the producing GEMM. n indexes output columns.
+ * packed_out (optional) receives to_bfp16 of the bf16 output (blocks of 8 output columns of a row) in packed_order,
+ * written by the GEMM's own epilogue: RL_ORDER_C_ATB, the reference GEMM's bfp16 C stream (M % 512 == 0, Nout %
+ * 1024 == 0; kernels/atb3/mm_bfp_mixed.cc:153-168), or RL_ORDER_A_LAYOUT, the next GEMM's A operand as the SwiGLU GEMM
+ * pushes H (M % 128 == 0, Nout % 64 == 0; kernels/atb3/mm_bfp_swiglu.cc:73-86). With packed_out, C may be NULL;
+ * otherwise C also receives the bf16 values (re-quantized with RL_EP_QUANTIZE_OUT, so they equal the packed blocks). */
 typedef struct rl_epilogue {
   int32_t act;               /* RL_ACT_* */
   int32_t flags;             /* RL_EP_* */
@@ -91,6 +107,9 @@ typedef struct rl_epilogue {
   int64_t gate_split_row;    /* 0 = every row uses gate row 0 */
   const uint16_t *residual;  /* bf16 (M, Nout) with leading dimension ld_residual, or NULL */
   int64_t ld_residual;
+  uint8_t *packed_out;       /* 9 * M * Nout / 8 bytes, 4-byte aligned, or NULL */
+  int32_t packed_order;      /* RL_ORDER_C_ATB or RL_ORDER_A_LAYOUT (when packed_out is set) */
+  int32_t c_order;           /* RL_C_ROWMAJOR or RL_C_ATB */
 } rl_epilogue;
 
 /* One GEMM. lda / ldc in elements (bf16); ldc >= Nout (N, or N/2 for SwiGLU). ep may be NULL (plain bf16 C).
@@ -113,10 +132,11 @@ int rl_bfp16_gemm(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_pa
  *     values, one HBM-bound pass: 9/8 + 2 bytes per value), and the product then runs on the RL_A_BF16 kernel with
  *     the rest of the workspace. The result is the RL_A_BF16 path's on the staged values: bit-identical to
  *     rl_bfp16_gemm's for the same format unless the K split applies.
- * workspace NULL: exactly rl_bfp16_gemm (a non-bf16 A then stages into a stream-ordered allocation).
- * workspace_bytes below what rl_bfp16_gemm_workspace_size() gives for the shape and format: RL_ERR_WORKSPACE for a
- * non-bf16 A that the staged copy does not fit; otherwise the planner runs whole K. Calls that share a workspace on
- * different streams race. Same reference interface as rl_bfp16_gemm (redline/forward.py:194-197). */
+ * workspace NULL: exactly rl_bfp16_gemm, which runs every shape and A format whole K (a non-bf16 A then stages into
+ * a stream-ordered allocation that holds the staged copy only, M * K * 2 bytes rounded up to 256).
+ * A workspace below rl_bfp16_gemm_workspace_size() for the shape and format (below the staged copy alone with
+ * RL_EP_WHOLE_K) returns RL_ERR_WORKSPACE before anything is enqueued (nothing is written to the workspace or C). Calls that share a workspace on different streams race.
+ * Same reference interface as rl_bfp16_gemm (redline/forward.py:194-197). */
 int rl_bfp16_gemm_ws(const void *A, int32_t a_fmt, int64_t lda, const uint8_t *B_packed, uint16_t *C, int64_t ldc,
                      int64_t M, int64_t N, int64_t K, const rl_epilogue *ep, void *workspace, int64_t workspace_bytes,
                      void *stream);

@@ -107,10 +107,29 @@ int rl_validate_gemm(int32_t a_fmt, int64_t lda, int64_t ldc, int64_t M, int64_t
   const int act = ep ? ep->act : RL_ACT_NONE;
   if (act != RL_ACT_NONE && act != RL_ACT_GELU_TANH && act != RL_ACT_SWIGLU)
     return fail(RL_ERR_ARG, "epilogue act %d unknown", act);
-  if (ep && (ep->flags & ~RL_EP_QUANTIZE_OUT)) return fail(RL_ERR_ARG, "epilogue flags 0x%x unknown", ep->flags);
+  if (ep && (ep->flags & ~(RL_EP_QUANTIZE_OUT | RL_EP_WHOLE_K)))
+    return fail(RL_ERR_ARG, "epilogue flags 0x%x unknown", ep->flags);
   const int64_t nout = act == RL_ACT_SWIGLU ? N / 2 : N;
-  if (ldc < nout || ldc % 8) return fail(RL_ERR_ALIGN, "ldc %lld: need >= %lld and a multiple of 8", (long long)ldc,
-                                          (long long)nout);
+  const int c_order = ep ? ep->c_order : RL_C_ROWMAJOR;
+  if (c_order != RL_C_ROWMAJOR && c_order != RL_C_ATB) return fail(RL_ERR_ARG, "c_order %d unknown", c_order);
+  if (c_order == RL_C_ATB && (M % 512 || nout % 1024))
+    return fail(RL_ERR_SHAPE, "a C in the ATB order needs M %% 512 == 0 and Nout %% 1024 == 0 (M %lld, Nout %lld)",
+                (long long)M, (long long)nout);
+  if (c_order == RL_C_ROWMAJOR && (ldc < nout || ldc % 8))
+    return fail(RL_ERR_ALIGN, "ldc %lld: need >= %lld and a multiple of 8", (long long)ldc, (long long)nout);
+  if (ep && ep->packed_out) {
+    if (ep->packed_order == RL_ORDER_C_ATB) {
+      if (M % 512 || nout % 1024)
+        return fail(RL_ERR_SHAPE, "packed C in the ATB order needs M %% 512 == 0 and Nout %% 1024 == 0 (M %lld, "
+                    "Nout %lld)", (long long)M, (long long)nout);
+    } else if (ep->packed_order == RL_ORDER_A_LAYOUT) {
+      if (M % 128 || nout % 64)
+        return fail(RL_ERR_SHAPE, "packed C in the A layout needs M %% 128 == 0 and Nout %% 64 == 0 (M %lld, "
+                    "Nout %lld)", (long long)M, (long long)nout);
+    } else {
+      return fail(RL_ERR_ARG, "packed_order %d: RL_ORDER_C_ATB or RL_ORDER_A_LAYOUT", ep->packed_order);
+    }
+  }
   switch (a_fmt) {
     case RL_A_BF16:
     case RL_A_BF16_QUANTIZE:

@@ -51,6 +51,10 @@ struct GemmDesc {
   int32_t tiles_m, tiles_n, tile_start;
   int32_t ksplit;  // K pieces: 1 = whole K; > 1 = each piece writes fp32 partials to `part`
   float* part;     // [ksplit][M][N] fp32 partial sums of the pieces, summed by gemm_reduce_kernel
+  uint8_t* pk;       // NULL, or the output's bfp16 blocks in pk_order (RL_ORDER_C_ATB or RL_ORDER_A_LAYOUT)
+  int32_t pk_order;
+  int32_t c_atb;     // C (if not NULL) is flat in the c_layout_atb(., 128, 128) element order instead of row major
+  int32_t prow;      // row of the whole output at this descriptor's row 0 (a second launch's rows start past it)
 };
 
 template <int G>
@@ -115,6 +119,85 @@ __device__ __forceinline__ u32x4 requantize8(u32x4 o) {
   return u32x4{r[0], r[1], r[2], r[3]};
 }
 
+// requantize8_fast that also returns the blocks' q bytes: q0..q3 in qw[0], q4..q7 in qw[1] (the low byte of each
+// encode_fast result is q in two's complement)
+__device__ __forceinline__ u32x4 requantize8_fast_q(u32x4 o, uint32_t E, uint32_t (&qw)[2]) {
+  const uint32_t w[4] = {o.x, o.y, o.z, o.w};
+  const BlockScale sc = block_scales(E);
+  const float off = -kMagic * sc.inv;
+  uint32_t r[4], qp[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const float flo = encode_fast(__uint_as_float(w[k] << 16), sc);
+    const float fhi = encode_fast(__uint_as_float(w[k] & 0xFFFF0000u), sc);
+    r[k] = pack_hi(decode_fast(flo, sc, off), decode_fast(fhi, sc, off));
+    qp[k] = __builtin_amdgcn_perm(__float_as_uint(fhi), __float_as_uint(flo), 0x0c0c0400u);
+  }
+  qw[0] = qp[0] | (qp[1] << 16);
+  qw[1] = qp[2] | (qp[3] << 16);
+  return u32x4{r[0], r[1], r[2], r[3]};
+}
+// the integer encoder of requantize8 with the q bytes as in requantize8_fast_q; not inlined: it serves only blocks of
+// extreme exponents (E < 8, E > 237), and inline it would take registers from every packed-output epilogue. The
+// result comes back by value (registers), not through memory.
+struct ReqQ {
+  u32x4 r;
+  uint32_t q0, q1;
+};
+__device__ __attribute__((noinline)) ReqQ requantize8_int_qv(u32x4 o) {
+  int32_t q[8];
+  const u32x4 r = quantize_bf16x8(o, nullptr, q);
+  return ReqQ{r, (q[0] & 0xFFu) | ((q[1] & 0xFFu) << 8) | ((q[2] & 0xFFu) << 16) | ((uint32_t)q[3] << 24),
+              (q[4] & 0xFFu) | ((q[5] & 0xFFu) << 8) | ((q[6] & 0xFFu) << 16) | ((uint32_t)q[7] << 24)};
+}
+__device__ __forceinline__ u32x4 requantize8_int_q(u32x4 o, uint32_t (&qw)[2]) {
+  const ReqQ t = requantize8_int_qv(o);
+  qw[0] = t.q0;
+  qw[1] = t.q1;
+  return t.r;
+}
+
+// Index of the block holding row r, columns c .. c + 7 (c % 8 == 0) of an (rows, nout) output in a packed order:
+//   RL_ORDER_C_ATB: c_layout_atb(., 128, 128) (redline/npu_layouts.py:42-47), blocks (rg, cg, col, row, sbr, sbc,
+//     br, bc, rib) with rg = r / 512, row = r / 128 % 4, sbr = r / 16 % 8, br = r / 8 % 2, rib = r % 8, cg = c / 1024,
+//     col = c / 128 % 8, sbc = c / 16 % 8, bc = c / 8 % 2 (nout % 1024 == 0);
+//   RL_ORDER_A_LAYOUT: a_layout(., 128, 64) (npu_layouts.py:18-22), blocks (mt, kt, sbr, bc, bis, rib) with
+//     mt = r / 128, kt = c / 64, sbr = r / 16 % 8, bc = c / 8 % 8, bis = r / 8 % 2, rib = r % 8 (nout % 64 == 0).
+// In both, rows 4j .. 4j + 3 of one 8-column block are 4 consecutive blocks (rib is the last digit).
+__device__ __forceinline__ int64_t out_block(int order, int r, int c, int nout) {
+  if (order == RL_ORDER_C_ATB) {
+    const int64_t g = (int64_t)(r >> 9) * (nout >> 10) + (c >> 10);
+    const int t = ((((((c >> 7) & 7) * 4 + ((r >> 7) & 3)) * 8 + ((r >> 4) & 7)) * 8 + ((c >> 4) & 7)) * 2 +
+                   ((r >> 3) & 1)) * 2 + ((c >> 3) & 1);
+    return (g * 8192 + t) * 8 + (r & 7);  // 8192 = 8 col x 4 row x 8 sbr x 8 sbc x 2 br x 2 bc
+  }
+  const int64_t g = (int64_t)(r >> 7) * (nout >> 6) + (c >> 6);
+  return ((g * 8 + ((r >> 4) & 7)) * 8 + ((c >> 3) & 7)) * 16 + (r & 15);
+}
+
+// The 8 bf16 of output block (row, col .. col + 7): row major, or 8 consecutive elements of the ATB element order
+__device__ __forceinline__ uint16_t* c_block(const GemmDesc& d, int row, int col, int nout) {
+  if (d.c_atb) return d.C + 8 * out_block(RL_ORDER_C_ATB, d.prow + row, col, nout);
+  return d.C + (int64_t)row * d.ldc + col;
+}
+
+// Four bfp16 blocks (exponents E[i], q0..q3 in ql[i], q4..q7 in qh[i]) as their 36 consecutive bytes
+// [E0 q0..q7][E1 ...][E2 ...][E3 ...], written as 9 dwords (p is 4-byte aligned: a block index that is a multiple
+// of 4 times 9 bytes)
+__device__ __forceinline__ void store_blocks4(uint8_t* p, const uint32_t (&E)[4], const uint32_t (&ql)[4],
+                                              const uint32_t (&qh)[4]) {
+  uint32_t* w = reinterpret_cast<uint32_t*>(p);
+  w[0] = E[0] | (ql[0] << 8);
+  w[1] = (ql[0] >> 24) | (qh[0] << 8);
+  w[2] = (qh[0] >> 24) | (E[1] << 8) | (ql[1] << 16);
+  w[3] = (ql[1] >> 16) | (qh[1] << 16);
+  w[4] = (qh[1] >> 16) | (E[2] << 16) | (ql[2] << 24);
+  w[5] = (ql[2] >> 8) | (qh[2] << 24);
+  w[6] = (qh[2] >> 8) | (E[3] << 24);
+  w[7] = ql[3];
+  w[8] = qh[3];
+}
+
 // Epilogue tile in LDS for 64 rows x 256 columns of fp32 accumulators, "row-quad" layout: the 4 values of rows
 // 4q..4q+3 of column c are 16 contiguous bytes at float index (q * 256 + slot(c)) * 4, so a lane writes one MFMA
 // accumulator (4 rows, one column) with one 16-byte store and a reader of 8 consecutive columns of 4 rows issues
@@ -128,7 +211,7 @@ __device__ __forceinline__ int ep_slot(int c) { return c ^ ((c >> 4) & 15); }
 
 // 8 values of one output block: bias, activation, gate / residual, bf16 rounding (RNE) and the optional bfp16
 // re-quantize, all in fp32; returns the 8 bf16 as 4 words.
-__device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int ocol, int nout, float (&v)[8]) {
+__device__ __forceinline__ u32x4 finish_bf16(const GemmDesc& d, int row, int ocol, int nout, float (&v)[8]) {
   if (d.gate || d.res) {
     f32x4 g4[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};  // NULL gate = 1
     if (d.gate) __builtin_memcpy(g4, d.gate + (row < d.gate_split ? nout : 0) + ocol, 32);
@@ -142,10 +225,36 @@ __device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int oc
       v[k] = rk + gk * v[k];
     }
   }
-  u32x4 o = {pack_bf16_rne(v[0], v[1]), pack_bf16_rne(v[2], v[3]), pack_bf16_rne(v[4], v[5]),
-             pack_bf16_rne(v[6], v[7])};
+  return u32x4{pack_bf16_rne(v[0], v[1]), pack_bf16_rne(v[2], v[3]), pack_bf16_rne(v[4], v[5]),
+               pack_bf16_rne(v[6], v[7])};
+}
+__device__ __forceinline__ u32x4 finish_block(const GemmDesc& d, int row, int ocol, int nout, float (&v)[8]) {
+  u32x4 o = finish_bf16(d, row, ocol, nout, v);
   if (d.flags & RL_EP_QUANTIZE_OUT) o = requantize8(o);
   return o;
+}
+
+// finish_block for an output that also goes out packed (d.pk): the bf16 block (re-quantized only with
+// RL_EP_QUANTIZE_OUT) and the packed block of the bf16 values, its exponent E and q bytes qw.
+__device__ __forceinline__ u32x4 finish_block_pk(const GemmDesc& d, int row, int ocol, int nout, float (&v)[8],
+                                                 uint32_t& E, uint32_t (&qw)[2]) {
+  const u32x4 o = finish_bf16(d, row, ocol, nout, v);
+  E = block_exp8(o);
+  // the float fast path when every lane's block allows it (a wave-uniform test), else the integer encoder for all
+  // lanes (it gives the fast path's bits wherever that applies)
+  u32x4 oq;
+  if (__builtin_amdgcn_ballot_w64(E < kFastEMin || E > kFastEMax) == 0)
+    oq = requantize8_fast_q(o, E, qw);
+  else
+    oq = requantize8_int_q(o, qw);
+  return (d.flags & RL_EP_QUANTIZE_OUT) ? oq : o;
+}
+
+// The 9 bytes of one packed block at p (any alignment)
+__device__ __forceinline__ void store_block1(uint8_t* p, uint32_t E, const uint32_t (&qw)[2]) {
+  p[0] = (uint8_t)E;
+#pragma unroll
+  for (int i = 0; i < 8; i++) p[1 + i] = (uint8_t)(qw[i >> 2] >> (8 * (i & 3)));
 }
 
 // Gate / residual, bf16 rounding and the optional re-quantize of rows row0..row0+3 of one 8-column block (v[i]:
@@ -201,7 +310,9 @@ __device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int oc
 // Second half of the GEMM epilogue. The LDS tile holds fp32 values (bias, activation and the SwiGLU product already
 // applied) of `nquads` row quads x W staged columns in the row-quad layout; staged column c is output column c0 + c.
 // Each thread takes blocks of 4 rows x 8 columns, one 16-byte store per row (the 4-wave kernel: finish_rows4).
-template <int W, int NTH = kG8ThreadsDecl>
+// kOut: the kernel variant for outputs in the reference's stream orders (d.pk, d.c_atb); without it those fields are
+// not read, and the code is that of a row-major bf16 C alone.
+template <int W, int NTH, bool kOut>
 __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, int r0, int c0, int nquads, int nout,
                                           int tid) {
   constexpr int kBlocks = W / 8;
@@ -215,6 +326,27 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
       f32x4 a[8];
 #pragma unroll
       for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * W + ep_slot(8 * cb + k)) * 4);
+      if (kOut && d.pk) {
+        // packed output: a row quad is all inside M or all past it (M % 128 == 0); the last M-tile of a launch can
+        // reach past M, and its quads there are skipped (their blocks would lie past the end of the packed stream).
+        // The four rows' blocks are 36 consecutive bytes.
+        if (r0 + 4 * q >= d.M) continue;
+        uint32_t E[4], ql[4], qh[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int row = r0 + 4 * q + i;
+          float v[8];
+#pragma unroll
+          for (int k = 0; k < 8; k++) v[k] = a[k][i];
+          uint32_t qw[2];
+          const u32x4 o = finish_block_pk(d, row, col, nout, v, E[i], qw);
+          ql[i] = qw[0];
+          qh[i] = qw[1];
+          if (d.C) *reinterpret_cast<u32x4*>(c_block(d, row, col, nout)) = o;
+        }
+        store_blocks4(d.pk + 9 * out_block(d.pk_order, d.prow + r0 + 4 * q, col, nout), E, ql, qh);
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int row = r0 + 4 * q + i;
@@ -223,7 +355,7 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
 #pragma unroll
         for (int k = 0; k < 8; k++) v[k] = a[k][i];
         const u32x4 o = finish_block(d, row, col, nout, v);
-        *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + col) = o;
+        *reinterpret_cast<u32x4*>(kOut ? c_block(d, row, col, nout) : d.C + (int64_t)row * d.ldc + col) = o;
       }
     }
     return;
@@ -236,6 +368,24 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
     f32x4 a[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * W + ep_slot(8 * cb + k)) * 4);
+    if (kOut && d.pk) {
+      // packed output, one row at a time (fewer live registers; the quad is inside M, checked above, and then all
+      // four rows are, M % 128 == 0): the four rows' blocks are 36 consecutive bytes of the packed order
+      uint32_t E[4], ql[4], qh[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = a[k][i];
+        uint32_t qw[2];
+        const u32x4 o = finish_block_pk(d, row0 + i, col, nout, v, E[i], qw);
+        ql[i] = qw[0];
+        qh[i] = qw[1];
+        if (d.C) *reinterpret_cast<u32x4*>(c_block(d, row0 + i, col, nout)) = o;
+      }
+      store_blocks4(d.pk + 9 * out_block(d.pk_order, d.prow + row0, col, nout), E, ql, qh);
+      continue;
+    }
     float v[4][8];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -243,10 +393,14 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
       for (int k = 0; k < 8; k++) v[i][k] = a[k][i];
     u32x4 o[4];
     finish_rows4(d, row0, col, nout, v, o);
-    uint16_t* const c = d.C + (int64_t)row0 * d.ldc + col;  // the other rows at uniform strides of ldc
+    if (kOut && !d.C) continue;
+    // row major: the other rows at uniform strides of ldc; the ATB element order: the next 8 elements (rib is the
+    // last block digit, and row0 % 4 == 0)
+    uint16_t* const c = kOut ? c_block(d, row0, col, nout) : d.C + (int64_t)row0 * d.ldc + col;
+    const int64_t rs = kOut && d.c_atb ? 8 : d.ldc;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      if (row0 + i < d.M) *reinterpret_cast<u32x4*>(c + i * d.ldc) = o[i];
+      if (row0 + i < d.M) *reinterpret_cast<u32x4*>(c + i * rs) = o[i];
   }
 }
 
@@ -307,8 +461,15 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const GemmDesc d) {
     else
       v[e] = d.act == RL_ACT_GELU_TANH ? gelu_tanh_f(x) : x;
   }
+  if (d.pk) {
+    uint32_t E, qw[2];
+    const u32x4 o = finish_block_pk(d, row, ocol, nout, v, E, qw);
+    store_block1(d.pk + 9 * out_block(d.pk_order, d.prow + row, ocol, nout), E, qw);
+    if (d.C) *reinterpret_cast<u32x4*>(c_block(d, row, ocol, nout)) = o;
+    return;
+  }
   const u32x4 o = finish_block(d, row, ocol, nout, v);
-  *reinterpret_cast<u32x4*>(d.C + (int64_t)row * d.ldc + ocol) = o;
+  *reinterpret_cast<u32x4*>(c_block(d, row, ocol, nout)) = o;
 }
 
 // ---- 8-wave kernel for bf16 A ---------------------------------------------------------------------------------
@@ -363,7 +524,7 @@ __device__ __forceinline__ void quarter_schedule() {
   __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
 }
 
-template <int G, int MF>
+template <int G, int MF, bool kOut>
 __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> args) {
   constexpr int TM = 32 * MF;                 // tile rows: MF 16-row fragments per wave, two waves down
   constexpr int kAS = TM * BK * 2;            // bytes of one A stage
@@ -636,7 +797,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
       }
     }
     __syncthreads();
-    ep8_finish<128>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
+    ep8_finish<128, kG8ThreadsDecl, kOut>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
   } else {
     const bool gelu = d.act == RL_ACT_GELU_TANH;
 #pragma unroll
@@ -658,7 +819,7 @@ __global__ __launch_bounds__(kG8Threads, 1) void gemm8_kernel(const GemmArgs<G> 
         }
       }
       __syncthreads();
-      ep8_finish<256>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
+      ep8_finish<256, kG8ThreadsDecl, kOut>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
       __syncthreads();
     }
   }
@@ -704,7 +865,7 @@ __device__ __forceinline__ void ep4_partial(const GemmDesc& d, const float* ep, 
   }
 }
 
-template <int G, int MF>
+template <int G, int MF, bool kOut>
 __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G> args) {
   static_assert(MF >= 4 && MF <= 8, "four decode octets per phase, 8 x 8 accumulators at most");
   constexpr int TM = 64 * MF;       // tile rows: 16 MF per wave, four waves down
@@ -943,7 +1104,7 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
     else
       swiglu_pass.template operator()<false>();
     __syncthreads();
-    ep8_finish<64, kW4Threads>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
+    ep8_finish<64, kW4Threads, kOut>(d, ep, m0, n0 / 2, TM / 4, nout, tid);
   } else {
     // bias and GELU chosen once per tile, so the staging loop has no per-value branches
     auto stage_pass = [&]<bool kBias, bool kGelu>() {
@@ -980,7 +1141,7 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
       if (part)
         ep4_partial(d, ep, m0 + TM / 2 * P, n0, TM / 8, piece, tid);
       else
-        ep8_finish<128, kW4Threads>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
+        ep8_finish<128, kW4Threads, kOut>(d, ep, m0 + TM / 2 * P, n0, TM / 8, nout, tid);
       __syncthreads();
     }
   }
@@ -991,7 +1152,10 @@ static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, 
                      int64_t N, int64_t K, const rl_epilogue* ep, int32_t a_fmt, int tile_start) {
   int s = rl_validate_gemm(a_fmt, lda, ldc, M, N, K, ep);
   if (s) return s;
-  if (!A || !B || !C) return fail(RL_ERR_NULL, "A, B or C is NULL");
+  if (!A || !B) return fail(RL_ERR_NULL, "A or B is NULL");
+  if (!C && !(ep && ep->packed_out)) return fail(RL_ERR_NULL, "C is NULL and there is no packed output");
+  if (ep && ep->packed_out && ((uintptr_t)ep->packed_out % 4))
+    return fail(RL_ERR_ALIGN, "packed_out must be 4-byte aligned");
   if ((a_fmt == RL_A_BF16 || a_fmt == RL_A_BF16_QUANTIZE) && ((uintptr_t)A % 16))
     return fail(RL_ERR_ALIGN, "bf16 A must be 16-byte aligned");
   if (a_fmt >= RL_A_PACKED_ROWBLOCK && ((uintptr_t)A % 4)) return fail(RL_ERR_ALIGN, "packed A must be 4-byte aligned");
@@ -1019,6 +1183,10 @@ static int fill_desc(GemmDesc& g, const void* A, int64_t lda, const uint8_t* B, 
   g.tile_start = tile_start;
   g.ksplit = 1;
   g.part = nullptr;
+  g.pk = ep ? ep->packed_out : nullptr;
+  g.pk_order = ep ? ep->packed_order : 0;
+  g.c_atb = ep && ep->c_order == RL_C_ATB;
+  g.prow = 0;
   return RL_OK;
 }
 
@@ -1194,17 +1362,31 @@ static void set_tiles8(GemmArgs<G>& args, int mf, int& total) {
   for (int i = args.n; i < G; i++) args.d[i] = args.d[args.n - 1];
 }
 
-template <int G>
-static int launch8(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+template <int G, bool kOut>
+static int launch8_v(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(total_tiles), block(kG8Threads);
   switch (mf) {
-    case 8: hipLaunchKernelGGL((gemm8_kernel<G, 8>), grid, block, 0, st, args); break;
-    case 7: hipLaunchKernelGGL((gemm8_kernel<G, 7>), grid, block, 0, st, args); break;
-    case 6: hipLaunchKernelGGL((gemm8_kernel<G, 6>), grid, block, 0, st, args); break;
-    default: hipLaunchKernelGGL((gemm8_kernel<G, 4>), grid, block, 0, st, args); break;
+    case 8: hipLaunchKernelGGL((gemm8_kernel<G, 8, kOut>), grid, block, 0, st, args); break;
+    case 7: hipLaunchKernelGGL((gemm8_kernel<G, 7, kOut>), grid, block, 0, st, args); break;
+    case 6: hipLaunchKernelGGL((gemm8_kernel<G, 6, kOut>), grid, block, 0, st, args); break;
+    default: hipLaunchKernelGGL((gemm8_kernel<G, 4, kOut>), grid, block, 0, st, args); break;
   }
   return launch_status("rl_bfp16_gemm");
+}
+
+// The kernel variant for the descriptors: the stream-order outputs (packed blocks, ATB-ordered C) compile into a
+// kernel of their own, so that the row-major kernels keep their register allocation.
+template <int G>
+static bool wants_out_variant(const GemmArgs<G>& args) {
+  for (int i = 0; i < args.n; i++)
+    if (args.d[i].pk || args.d[i].c_atb) return true;
+  return false;
+}
+template <int G>
+static int launch8(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+  return wants_out_variant(args) ? launch8_v<G, true>(args, total_tiles, mf, stream)
+                                 : launch8_v<G, false>(args, total_tiles, mf, stream);
 }
 
 // Tiles of the 4-wave kernel: 64 mf rows x 128 columns (one b_layout N-tile), times the K pieces.
@@ -1221,24 +1403,30 @@ static void set_tiles4w(GemmArgs<G>& args, int mf, int& total) {
   for (int i = args.n; i < G; i++) args.d[i] = args.d[args.n - 1];
 }
 
-template <int G>
-static int launch4w(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+template <int G, bool kOut>
+static int launch4w_v(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(total_tiles), block(kW4Threads);
   switch (mf) {
-    case 8: hipLaunchKernelGGL((gemm4w_kernel<G, 8>), grid, block, 0, st, args); break;
-    case 7: hipLaunchKernelGGL((gemm4w_kernel<G, 7>), grid, block, 0, st, args); break;
-    case 6: hipLaunchKernelGGL((gemm4w_kernel<G, 6>), grid, block, 0, st, args); break;
-    default: hipLaunchKernelGGL((gemm4w_kernel<G, 4>), grid, block, 0, st, args); break;
+    case 8: hipLaunchKernelGGL((gemm4w_kernel<G, 8, kOut>), grid, block, 0, st, args); break;
+    case 7: hipLaunchKernelGGL((gemm4w_kernel<G, 7, kOut>), grid, block, 0, st, args); break;
+    case 6: hipLaunchKernelGGL((gemm4w_kernel<G, 6, kOut>), grid, block, 0, st, args); break;
+    default: hipLaunchKernelGGL((gemm4w_kernel<G, 4, kOut>), grid, block, 0, st, args); break;
   }
   return launch_status("rl_bfp16_gemm");
+}
+template <int G>
+static int launch4w(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+  return wants_out_variant(args) ? launch4w_v<G, true>(args, total_tiles, mf, stream)
+                                 : launch4w_v<G, false>(args, total_tiles, mf, stream);
 }
 
 // The descriptor of rows R.. of a GEMM.
 static GemmDesc rows_from(const GemmDesc& g, int64_t R) {
   GemmDesc t = g;
   t.A = static_cast<const uint16_t*>(g.A) + R * g.lda;
-  t.C = g.C + R * g.ldc;
+  t.C = g.C && !g.c_atb ? g.C + R * g.ldc : g.C;  // packed and ATB positions come from prow
+  t.prow = (int32_t)(g.prow + R);
   if (g.res) t.res = g.res + R * g.ldr;
   t.M = (int32_t)(g.M - R);
   t.gate_split = (int32_t)(g.gate_split > R ? g.gate_split - R : 0);
@@ -1342,20 +1530,24 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
   args.n = 1;
   if ((s = check_device())) return s;
   if (a_fmt != RL_A_BF16) {
+    // stage A as bf16 (its bfp16 values) at the start of the workspace, then run the bf16 path with the rest of it
+    const int64_t sa = staged_a_bytes(M, K);
     if (!workspace) {
-      // no workspace: the same call on a stream-ordered allocation of the size this format and shape use
-      const int64_t need = rl_bfp16_gemm_workspace_size(a_fmt, M, N, K);
+      // no workspace: the staged copy alone goes into a stream-ordered allocation and the product runs whole K, so
+      // rl_bfp16_gemm gives every A format the bits of the RL_A_BF16 call on the same values
       void* tmp = nullptr;
-      if ((s = stream_alloc(&tmp, need, stream))) return s;
-      s = rl_bfp16_gemm_ws(A, a_fmt, lda, B_packed, C, ldc, M, N, K, ep, tmp, need, stream);
+      if ((s = stream_alloc(&tmp, sa, stream))) return s;
+      uint16_t* a16 = static_cast<uint16_t*>(tmp);
+      s = stage_a(A, a_fmt, lda, M, K, a16, stream);
+      if (!s) s = rl_bfp16_gemm_ws(a16, RL_A_BF16, K, B_packed, C, ldc, M, N, K, ep, nullptr, 0, stream);
       return stream_free(tmp, stream, s);
     }
-    // stage A as bf16 (its bfp16 values) at the start of the workspace, then run the bf16 path with the rest of
-    // the workspace
-    const int64_t sa = staged_a_bytes(M, K);
-    if (workspace_bytes < sa)
-      return fail(RL_ERR_WORKSPACE, "workspace %lld bytes, staging A needs %lld (rl_bfp16_gemm_workspace_size)",
-                  (long long)workspace_bytes, (long long)sa);
+    // the whole workspace (the staged copy, then any K-split partials) is checked before anything is enqueued
+    const bool whole = ep && (ep->flags & RL_EP_WHOLE_K);
+    const int64_t need = sa + (whole ? 0 : plan_split(M, N, K, device_cus()).ws_bytes);
+    if (workspace_bytes < need)
+      return fail(RL_ERR_WORKSPACE, "workspace %lld bytes, this shape and A format need %lld "
+                  "(rl_bfp16_gemm_workspace_size)", (long long)workspace_bytes, (long long)need);
     uint16_t* a16 = static_cast<uint16_t*>(workspace);
     if ((s = stage_a(A, a_fmt, lda, M, K, a16, stream))) return s;
     const int64_t rest = workspace_bytes - sa;
@@ -1363,7 +1555,7 @@ int rl_bfp16_gemm_ws(const void* A, int32_t a_fmt, int64_t lda, const uint8_t* B
                             rest > 0 ? static_cast<uint8_t*>(workspace) + sa : nullptr, rest, stream);
   }
   int total = 0;
-  if (workspace) {
+  if (workspace && !(ep && (ep->flags & RL_EP_WHOLE_K))) {
     const SplitPlan sp = plan_split(M, N, K, device_cus());
     if (sp.ks > 1) {
       if (sp.ws_bytes > workspace_bytes)

@@ -17,7 +17,8 @@ RL_ORDER_ROWBLOCK, RL_ORDER_A_LAYOUT, RL_ORDER_B_LAYOUT, RL_ORDER_C_ATB = 0, 1, 
 RL_A_BF16, RL_A_BF16_QUANTIZE, RL_A_PACKED_ROWBLOCK, RL_A_PACKED_A_LAYOUT = 0, 1, 2, 3
 RL_ACT_NONE, RL_ACT_GELU_TANH, RL_ACT_SWIGLU = 0, 1, 2
 RL_GEMV_SILU = 3
-RL_EP_QUANTIZE_OUT = 1
+RL_EP_QUANTIZE_OUT, RL_EP_WHOLE_K = 1, 2
+RL_C_ROWMAJOR, RL_C_ATB = 0, 1
 RL_NORM_LAYER, RL_NORM_RMS = 0, 1
 RL_BRANCH_BF16, RL_BRANCH_PACKED = 0, 1
 RL_MAX_GROUP = 16
@@ -38,7 +39,8 @@ class RLError(RuntimeError):
 class Epilogue(ctypes.Structure):
     _fields_ = [("act", ctypes.c_int32), ("flags", ctypes.c_int32), ("bias", ctypes.c_void_p),
                 ("gate", ctypes.c_void_p), ("gate_split_row", ctypes.c_int64), ("residual", ctypes.c_void_p),
-                ("ld_residual", ctypes.c_int64)]
+                ("ld_residual", ctypes.c_int64), ("packed_out", ctypes.c_void_p), ("packed_order", ctypes.c_int32),
+                ("c_order", ctypes.c_int32)]
 
 
 class GemmDesc(ctypes.Structure):

@@ -159,16 +159,15 @@ class NPU:
         if c.dtype == torch.bfloat16 and c.dim() == 2:
             ops.gemm(a, b, N, K, M=M, a_fmt=fmt, act=act, out=c.view(M, nout))
             return
-        y = ops.gemm(a, b, N, K, M=M, a_fmt=fmt, act=act)
         if c.dtype == torch.bfloat16:
-            # flat bf16 C: the C16 artifacts' element order (kernels/vlm/mm_bfp_c16.cc:1-2)
+            # flat bf16 C: the C16 artifacts' element order (kernels/vlm/mm_bfp_c16.cc:1-2), written by the epilogue
             if act:
                 raise ValueError("the SwiGLU GEMM writes H as a V9 stream or a 2-D bf16 tensor")
-            c.copy_(layouts.c_layout_atb_values(y))
+            ops.gemm(a, b, N, K, M=M, a_fmt=fmt, out=c, c_order="c_atb")
             return
-        # V9 output: the reference's stream order, from the bf16 result
-        p, _ = ops.quantize(y, order="a_layout" if act else "c_atb")
-        c.copy_(p)
+        # V9 output: the reference's stream order (the ATB C stream, or H in the down GEMM's A layout), written as
+        # bfp16 blocks by the GEMM's own epilogue (kernels/atb3/mm_bfp_mixed.cc:153-168, mm_bfp_swiglu.cc:73-86)
+        ops.gemm(a, b, N, K, M=M, a_fmt=fmt, act=act, packed_out=c, packed_order="a_layout" if act else "c_atb")
 
     def report(self):
         tot_w, tot_n = sum(self.t_wall.values()), sum(self.t_npu.values())

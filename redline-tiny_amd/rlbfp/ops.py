@@ -154,14 +154,23 @@ def staged_a_bytes(M, K):
     return (M * K * 2 + 255) // 256 * 256
 
 
+PACKED_ORDERS = {"c_atb": L.RL_ORDER_C_ATB, "a_layout": L.RL_ORDER_A_LAYOUT}
+C_ORDERS = {"rowmajor": L.RL_C_ROWMAJOR, "c_atb": L.RL_C_ATB}
+
+
 def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None, gate_split_row=0,
-         residual=None, quantize_out=False, out=None, split=True, workspace=True):
+         residual=None, quantize_out=False, out=None, split=True, workspace=True, packed_out=None,
+         packed_order="c_atb", c_order="rowmajor"):
     """C = epilogue(A @ B) with B the packed weight stream of a (K, N) matrix, bf16 output (M, N) (or (M, N/2) for
     act="swiglu"). See rl_bfp16_gemm in include/rlbfp.h for the epilogue order. split: let a small-M, deep-K GEMM
     split K into pieces (rl_bfp16_gemm_ws, workspace from torch's allocator); False: always whole K. An A format
     other than "bf16" is decoded (or quantized) into a bf16 copy first, then the bf16 kernel runs; workspace: that
     copy (and any K split) lives in a workspace from torch's allocator; False: rl_bfp16_gemm takes a stream-ordered
-    allocation of its own (not allowed under graph capture)."""
+    allocation of its own (not allowed under graph capture).
+    packed_out: a uint8 tensor of 9 M Nout / 8 bytes that the epilogue fills with to_bfp16 of the bf16 output in
+    packed_order ("c_atb": the reference GEMM's C stream; "a_layout": the next GEMM's A, as the SwiGLU GEMM writes H);
+    with packed_out and no out, no bf16 C is written and packed_out is returned. c_order="c_atb": the bf16 C is flat
+    (M * Nout values) in the c_layout_atb element order (the C16 artifacts' output)."""
     _dev(a, "A")
     _dev(b_packed, "B")
     if M is None:
@@ -172,26 +181,51 @@ def gemm(a, b_packed, N, K, M=None, a_fmt="bf16", act=None, bias=None, gate=None
     if b_packed.dtype != torch.uint8 or b_packed.numel() != packed_bytes(K, N):
         raise ValueError(f"B must be a uint8 stream of {packed_bytes(K, N)} bytes")
     nout = N // 2 if act == "swiglu" else N
-    if out is None:
-        out = torch.empty((M, nout), dtype=torch.bfloat16, device=a.device)
-    elif out.dtype != torch.bfloat16 or out.shape != (M, nout) or out.stride(1) != 1:
-        raise ValueError(f"out must be ({M}, {nout}) bfloat16 with unit column stride")
+    if packed_out is not None:
+        _dev(packed_out, "packed_out")
+        if packed_out.dtype != torch.uint8 or not packed_out.is_contiguous() or \
+                packed_out.numel() != packed_bytes(M, nout):
+            raise ValueError(f"packed_out must be a contiguous uint8 tensor of {packed_bytes(M, nout)} bytes")
+        if packed_order not in PACKED_ORDERS:
+            raise ValueError(f"packed_order must be one of {sorted(PACKED_ORDERS)}")
+    if c_order not in C_ORDERS:
+        raise ValueError(f"c_order must be one of {sorted(C_ORDERS)}")
+    no_c = out is None and packed_out is not None
+    if c_order == "c_atb":
+        if out is None and not no_c:
+            out = torch.empty(M * nout, dtype=torch.bfloat16, device=a.device)
+        if out is not None and (out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != M * nout):
+            raise ValueError(f"out in the ATB order must be a contiguous bfloat16 tensor of {M * nout} values")
+        ldc = nout
+    else:
+        if out is None and not no_c:
+            out = torch.empty((M, nout), dtype=torch.bfloat16, device=a.device)
+        if out is not None and (out.dtype != torch.bfloat16 or out.shape != (M, nout) or out.stride(1) != 1):
+            raise ValueError(f"out must be ({M}, {nout}) bfloat16 with unit column stride")
+        ldc = out.stride(0) if out is not None else nout
     _check_ep_sizes(M, N, nout, bias, gate, gate_split_row, residual)
     ep = _epilogue(act, bias, gate, gate_split_row, residual, quantize_out)
+    if packed_out is not None:
+        ep.packed_out = packed_out.data_ptr()
+        ep.packed_order = PACKED_ORDERS[packed_order]
+    ep.c_order = C_ORDERS[c_order]
+    c_ptr = ctypes.c_void_p(out.data_ptr()) if out is not None else None
     if not workspace:
         nws = 0
     elif a_fmt == "bf16":
         nws = gemm_workspace_bytes(M, N, K, a.device) if split else 0
     else:
         nws = gemm_workspace_bytes(M, N, K, a.device, a_fmt) if split else staged_a_bytes(M, K)
+    if nws and not split:
+        ep.flags |= L.RL_EP_WHOLE_K  # a non-bf16 A staged in the workspace, the product whole K
     if nws:
         ws = torch.empty(nws, dtype=torch.uint8, device=a.device)
-        L.check(L.lib().rl_bfp16_gemm_ws(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M,
-                                         N, K, ctypes.byref(ep), _ptr(ws), nws, _stream(a)))
+        L.check(L.lib().rl_bfp16_gemm_ws(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), c_ptr, ldc, M, N, K,
+                                         ctypes.byref(ep), _ptr(ws), nws, _stream(a)))
     else:
-        L.check(L.lib().rl_bfp16_gemm(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), _ptr(out), out.stride(0), M, N,
-                                      K, ctypes.byref(ep), _stream(a)))
-    return out
+        L.check(L.lib().rl_bfp16_gemm(_ptr(a), A_FORMATS[a_fmt], lda, _ptr(b_packed), c_ptr, ldc, M, N, K,
+                                      ctypes.byref(ep), _stream(a)))
+    return out if out is not None else packed_out
 
 
 class GemmSpec:

@@ -49,9 +49,10 @@ def test_validate_quantize(args, code):
         assert L.lib().rl_last_error().decode()
 
 
-def ep(act=0, flags=0, residual=None, ld=0, split=0):
+def ep(act=0, flags=0, residual=None, ld=0, split=0, packed=None, order=0, c_order=0):
     e = L.Epilogue()
     e.act, e.flags, e.residual, e.ld_residual, e.gate_split_row = act, flags, residual, ld, split
+    e.packed_out, e.packed_order, e.c_order = packed, order, c_order
     return ctypes.byref(e)
 
 
@@ -71,6 +72,17 @@ def ep(act=0, flags=0, residual=None, ld=0, split=0):
     (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(flags=4), L.RL_ERR_ARG),
     (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(residual=1, ld=100), L.RL_ERR_SHAPE),
     (L.RL_A_BF16, 3072, 3072, 64, 3072, 3072, ep(split=-1), L.RL_ERR_ARG),
+    # packed output in the reference's stream orders: ATB C (M % 512, Nout % 1024), A layout (M % 128, Nout % 64)
+    (L.RL_A_BF16, 3072, 9216, 4608, 9216, 3072, ep(packed=16, order=L.RL_ORDER_C_ATB), L.RL_OK),
+    (L.RL_A_BF16, 3072, 9216, 4352, 9216, 3072, ep(packed=16, order=L.RL_ORDER_C_ATB), L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3072, 12288, 4352, 24576, 3072, ep(L.RL_ACT_SWIGLU, packed=16, order=L.RL_ORDER_A_LAYOUT),
+     L.RL_OK),
+    (L.RL_A_BF16, 3072, 12288, 4300, 24576, 3072, ep(L.RL_ACT_SWIGLU, packed=16, order=L.RL_ORDER_A_LAYOUT),
+     L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3072, 3072, 512, 3072, 3072, ep(packed=16, order=L.RL_ORDER_ROWBLOCK), L.RL_ERR_ARG),
+    (L.RL_A_BF16, 3072, 0, 512, 3072, 3072, ep(c_order=L.RL_C_ATB), L.RL_OK),  # ldc ignored
+    (L.RL_A_BF16, 3072, 3072, 256, 3072, 3072, ep(c_order=L.RL_C_ATB), L.RL_ERR_SHAPE),
+    (L.RL_A_BF16, 3072, 3072, 512, 3072, 3072, ep(c_order=2), L.RL_ERR_ARG),
 ])
 def test_validate_gemm(a_fmt, lda, ldc, M, N, K, e, code):
     assert L.lib().rl_validate_gemm(a_fmt, lda, ldc, M, N, K, e) == code

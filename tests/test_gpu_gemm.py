@@ -59,15 +59,19 @@ def test_output_canary_and_ldc(dev):
     assert (big[:, N:] == 7.0).all() and (big[M:, :] == 7.0).all()
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 192, 256), (128, 4096, 384)])
 @pytest.mark.parametrize("workspace", [True, False])
 @pytest.mark.parametrize("a_fmt", ["bf16_quantize", "packed_rowblock", "packed_a_layout"])
-def test_a_formats_agree(dev, a_fmt, workspace):
+def test_a_formats_agree(dev, a_fmt, workspace, M, K, N):
     """Every A format computes on the same bfp16 values: results identical to the bf16 (pre-quantized) path, whether
-    the staged bf16 copy of A lives in the caller's workspace or in the library's own stream-ordered allocation."""
-    M, K, N = 256, 192, 256
+    the staged bf16 copy of A lives in the caller's workspace or in the library's own stream-ordered allocation.
+    128 x 4096 x 384 is a shape the planner splits along K when given a workspace: with one, every format runs the
+    split (the bf16 path's split bits); without one (rl_bfp16_gemm), every format runs whole K (its whole-K bits)."""
     rng, A, packed, Aq, Bq = setup(M, K, N, 4, outliers=0.01)
     b = dev_t(packed, torch.uint8)
-    ref = ops.gemm(dev_t(Aq, torch.bfloat16), b, N, K)
+    if K == 4096:
+        assert ops.gemm_workspace_bytes(M, N, K) > 0, "the case is meant to split"
+    ref = ops.gemm(dev_t(Aq, torch.bfloat16), b, N, K, split=workspace)
     if a_fmt == "bf16_quantize":
         a = dev_t(A, torch.bfloat16)
     elif a_fmt == "packed_rowblock":
@@ -303,6 +307,38 @@ def test_k_split_workspace(dev):
     assert L.lib().rl_bfp16_gemm_ws(*args, None, 0, st) == 0
     torch.cuda.synchronize()
     assert torch.equal(out, ops.gemm(a, b, N, K, split=False))
+
+
+def test_workspace_checked_before_staging(dev):
+    """A non-bf16 A with a workspace that holds the staged bf16 copy but not the K-split partials: RL_ERR_WORKSPACE,
+    returned before anything is enqueued, so neither the workspace nor C is written (both keep their canary bytes);
+    the same call with rl_bfp16_gemm_workspace_size bytes then runs (the bf16 path's split bits)."""
+    from rlbfp import _lib as L
+    M, K, N = 100, 4096, 384
+    rng = np.random.default_rng(29)
+    A = G.activations(rng, M, K)
+    packed = F.pack_b(G.linear_weight(rng, N, K).T)
+    Aq, Bq = F.quantize_rows(A), F.decode_b(packed, K, N)
+    a = dev_t(F.to_bfp16(A.reshape(-1)), torch.uint8)  # packed row blocks: the values of Aq
+    b = dev_t(packed, torch.uint8)
+    lib = L.lib()
+    need = lib.rl_bfp16_gemm_workspace_size(L.RL_A_PACKED_ROWBLOCK, M, N, K)
+    staged = ops.staged_a_bytes(M, K)
+    assert need > staged + 16 and lib.rl_bfp16_gemm_workspace_bytes(M, N, K) == need - staged
+    ws = torch.full((need,), 0xA5, dtype=torch.uint8, device="cuda")
+    out = torch.full((M, N), 3.0, dtype=torch.bfloat16, device="cuda")
+    ep = ops._epilogue(None, None, None, 0, None, False)
+    st = torch.cuda.current_stream().cuda_stream
+    args = (a.data_ptr(), L.RL_A_PACKED_ROWBLOCK, K, b.data_ptr(), out.data_ptr(), N, M, N, K, ctypes.byref(ep))
+    for short in (need - 16, staged, staged - 256):
+        assert lib.rl_bfp16_gemm_ws(*args, ws.data_ptr(), short, st) == L.RL_ERR_WORKSPACE, short
+    torch.cuda.synchronize()
+    assert bool((ws == 0xA5).all()), "the refused call wrote to the workspace"
+    assert bool((out == 3.0).all()), "the refused call wrote to C"
+    assert lib.rl_bfp16_gemm_ws(*args, ws.data_ptr(), need, st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, ops.gemm(dev_t(Aq, torch.bfloat16), b, N, K))
+    check(out, G.gemm_ref(Aq, Bq))
 
 
 def _exponent_class_weight(rng, N, K, classes):

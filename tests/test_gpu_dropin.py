@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from dropin_check import (RecordingNPU, check_attn, check_gemm, check_ln, check_qkv_post, close_values, host,
+from dropin_check import (TILE9, RecordingNPU, check_attn, check_gemm, check_ln, check_qkv_post, close_values, host,
                           stream_values)
 from oracle import bfp16 as F
 from oracle import gemm as G
@@ -122,6 +122,69 @@ def test_cached_step_blocks(dev):
     seen = check_log(npu.log, cos, sin, lambda a: meta, "layer")
     assert seen == {"img_in", "ln_mod", "qkv", "qkv_post", "attn", "o", "up_swiglu", "down", "proj_out"}
     assert npu.calls["qkv"] == 2 and npu.calls["ln_mod"] == 5
+
+
+def test_extract_step_blocks(dev):
+    """ExtractStep.blocks' op list for one block (redline/forward.py:362-388) through NPU.run at 1024 rows x 1024
+    hidden (8 heads), FFN 2048, on the reference's V9 and flat bf16 buffers: qkv, qkv_post, the step-1 attention
+    ("attn" for the target Q tiles 8..15 over their own keys and the prefix tiles 0..7 with 40 padded keys, "attn_ref"
+    for Q tiles 0..7 over the prefix, "attn_small" for one 64-query group with per-row key limits), o, ln_mod with the
+    step-1 parameter split (glue-ln-m1024-s3: rows below 384 take parameter row 1, as glue-ln-m8704-s33 does at
+    M = 8704), up_swiglu, down and the closing ln_mod. Every op is checked against the oracle on the inputs it was
+    given. The host-side merge of the small-query rows (ExtractStep._small_q / _merge_small) is orchestration, not a
+    device op, and is not replayed."""
+    rng = np.random.default_rng(4)
+    M, HID, FF, H = 1024, 1024, 2048, 8
+    T = M // 64
+    mats = {(0, "qkv"): F.pack_b(G.linear_weight(rng, 3 * HID, HID).T),
+            (0, "o"): F.pack_b(G.linear_weight(rng, HID, HID).T),
+            (0, "up"): F.pack_b(F.interleave_up(G.linear_weight(rng, FF, HID), G.linear_weight(rng, FF, HID))),
+            (0, "down"): F.pack_b(G.linear_weight(rng, HID, FF).T)}
+    w = FW.Weights.from_tensors({k: cuda(v) for k, v in mats.items()})
+    w.b[0, "norm_q"] = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    w.b[0, "norm_k"] = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    cos, sin = rope_tables(rng, M)
+    # the buffers and per-step parameters of a step at M rows (CachedStep allocates the same V9 / flat bf16 set)
+    ex = FW.CachedStep(w, cos, sin, None, M=M, n_blocks=1)
+    wqc = F.bf16_round(w.b[0, "norm_q"].astype(np.float32) * np.float32(QK.C_LOG2))
+    remember_tables(ex.tabs[0], wqc, F.bf16_round(w.b[0, "norm_k"]))
+    ex.set_t(0.3 * rng.standard_normal((2, 4 * HID)), 0.2 * rng.standard_normal((2, HID)))
+    x0 = F.bf16_round(rng.standard_normal((M, HID)).astype(np.float32) * 2)
+    ex.x[0].copy_(cuda(F.c_layout_atb(x0), torch.bfloat16))
+    ex.a.copy_(cuda(F.to_bfp16(F.a_layout(rng.standard_normal((M, HID)).astype(np.float32)))))
+    npu = RecordingNPU()
+    pad = 40
+    metas = {
+        "s1": {"family": "attn32o", "H": H, "QN": 8, "NK": 16 * 64, "NKV": 16 * 64 - pad, "OA": 1, "OHEADS": H,
+               "H0": 0, "KVSPLIT": 8, "QT": T, "Q0": 8, "KT": T, "K0": 8, "PT": T, "P0": 0},
+        "ref": {"family": "attn32o", "H": H, "QN": 8, "NK": 8 * 64, "NKV": 8 * 64 - pad, "OA": 1, "OHEADS": H,
+                "H0": 0, "QT": T, "Q0": 0, "KT": T, "K0": 0},
+        "small": {"family": "attn32q", "H": H, "NK": 8 * 64, "PT": T, "P0": 0, "OA": 1, "OHEADS": H, "H0": 0}}
+    npu.meta.update(metas)
+    strip = 128 * HID // 8 * 9                      # one 128-row strip of O (A layout)
+    o_tgt, o_ref = ex.o[4 * strip:8 * strip], ex.o[:4 * strip]
+    ln_art = "glue-ln-m1024-s3"
+    # the block's op list, in ExtractStep.blocks' order
+    FW.gemm(npu, w, "qkv", M, ex.a, ex.c_qkv, block=0)
+    npu.run("qkv_post", "glue-qkv32-m1024", [ex.c_qkv, ex.tabs[0], ex.q, ex.kv])
+    npu.run("attn", "s1", [ex.q, ex.kv, ex.kv, o_tgt])
+    npu.run("attn_ref", "ref", [ex.q, ex.kv, o_ref])
+    q_small = ex.q.reshape(H, T, TILE9)[:, 9:10].contiguous().reshape(-1)   # one query tile per head (rows 576..639)
+    lim = np.concatenate([np.arange(16), rng.integers(0, 8 * 64 - pad - 1, 48)]).astype(np.int32)
+    lim_buf = np.zeros(64 * 64 // 8 * 9, np.uint8)
+    lim_buf[:256] = lim.view(np.uint8)
+    o_small = FW.v9(128 * HID)
+    npu.run("attn_small", "small", [q_small, cuda(lim_buf), ex.kv, o_small])
+    FW.gemm(npu, w, "o", M, ex.o, ex.c, block=0)
+    npu.run("ln_mod", ln_art, [ex.x[0], ex.c, ex.p_mlp, ex.x[1], ex.a])
+    npu.run("up_swiglu", "atb3sw2-m1024", [ex.a, w.b[0, "up"], ex.h])
+    FW.gemm(npu, w, "down", M, ex.h, ex.c, block=0)
+    npu.run("ln_mod", ln_art, [ex.x[1], ex.c, ex.p_out, ex.x[0], ex.a])
+    seen = check_log(npu.log, cos, sin, lambda art: metas[art], "layer")
+    assert seen == {"qkv", "qkv_post", "attn", "attn_ref", "attn_small", "o", "ln_mod", "up_swiglu", "down"}
+    # the parameter split really splits: rows below 384 and above it were normalised with different parameters
+    lp = np.asarray(host(ex.p_mlp)).reshape(2, -1)
+    assert not np.array_equal(lp[0], lp[1])
 
 
 class _VlmW:
@@ -236,10 +299,11 @@ def test_step1_attention_artifacts(dev):
 
 @pytest.mark.parametrize("M,K,N", [(4096, 3072, 3072), (512, 12288, 4096)])
 def test_v9_a_staged_fast_path(dev, M, K, N):
-    """A in the NPU's A layout (decoded to bf16, then the bf16 kernel): the same bits whether the bf16 copy lives in
-    a workspace from torch or in the library's own stream-ordered allocation; whole K, the bits of the bf16-A GEMM
-    on the decoded values (the 512 x 12288 shape otherwise splits K); all meet the oracle on sampled rows. The first
-    shape is config 1's, the second the text encoder's down projection."""
+    """A in the NPU's A layout (decoded to bf16, then the bf16 kernel). With a workspace from torch the call gets the
+    bf16-A GEMM's bits on the decoded values, K split where the planner splits (the 512 x 12288 shape); in the
+    library's own stream-ordered allocation (rl_bfp16_gemm, no workspace) and with split=False (RL_EP_WHOLE_K) it runs
+    whole K, the bits of the whole-K bf16-A GEMM. All meet the oracle on sampled rows. The first shape is config 1's,
+    the second the text encoder's down projection."""
     rng = np.random.default_rng(M + K)
     A = G.activations(rng, M, K)
     W = G.linear_weight(rng, N, K)
@@ -249,7 +313,8 @@ def test_v9_a_staged_fast_path(dev, M, K, N):
     own = ops.gemm(a, b, N, K, M=M, a_fmt="packed_a_layout", workspace=False)
     whole = ops.gemm(a, b, N, K, M=M, a_fmt="packed_a_layout", split=False)
     a16 = ops.dequantize(a, M, K, order="a_layout", dtype=torch.bfloat16)
-    assert torch.equal(own, fast)
+    assert torch.equal(fast, ops.gemm(a16, b, N, K))
+    assert torch.equal(own, whole)
     assert torch.equal(whole, ops.gemm(a16, b, N, K, split=False))
     rows = np.sort(rng.choice(M, 128, replace=False))
     Aq = F.quantize_rows(A[rows])

@@ -125,6 +125,12 @@ def decode_kv(buf, heads, t_all, t0, n):
     return k, v
 
 
+def _kv_rows(buf, heads):
+    """Every token row of a [head][tiles][K | V][tile] buffer: (K, V), each (heads, 64 tiles, 128)."""
+    t_all = buf.numel() // (heads * 2 * TILE9)
+    return decode_kv(buf, heads, t_all, 0, t_all)
+
+
 def check_attn(meta, before, after):
     """O of an attention artifact against the oracle on its decoded tiles; blocks of O it does not own unchanged."""
     o_before, o_after = host(before[-1]).reshape(-1, 9), host(after[-1]).reshape(-1, 9)
@@ -140,27 +146,36 @@ def check_attn(meta, before, after):
         ref = AT.attention_ref(q, np.repeat(k, g, 0), np.repeat(v, g, 0), lim=np.arange(n))
         rows_all, cols_all, h0, nrows = Mr, hq * 128, 0, n
     elif fam == "attn32q":
-        H, nkt = meta.get("H", 32), meta["NK"] // 64
+        # one 64-query tile per head; keys = token rows [64 P0, 64 P0 + NK) of the KV buffer, whose tiles per head
+        # come from its size
+        H, nk = meta.get("H", 32), meta["NK"]
         q = decode_q(before[0], H, 1, 0, 1)
         lim = host(before[1]).reshape(-1)[:256].view(np.int32)
-        k, v = decode_kv(before[2], H, meta.get("PT") or nkt, meta.get("P0", 0), nkt)
-        ref = AT.attention_ref(q, k, v, lim=lim)
+        k_all, v_all = _kv_rows(before[2], H)
+        r0 = 64 * meta.get("P0", 0)
+        assert r0 + nk <= k_all.shape[1]
+        ref = AT.attention_ref(q, k_all[:, r0:r0 + nk], v_all[:, r0:r0 + nk], lim=lim)
         rows_all, cols_all, h0, nrows = 128, meta.get("OHEADS", 32) * 128, meta.get("H0", 0), 64
     else:
+        # token rows, from the artifact's offsets and each buffer's own size (kernels/attn/attn_design.py:235-240):
+        # queries [64 Q0, 64 (Q0 + QN)) of the Q buffer; keys [64 K0, 64 K0 + n1) of the first KV buffer, then
+        # [64 P0, 64 P0 + NK - n1) of the second, n1 = 64 KVSPLIT (all NK keys from the first without a split)
         H, nk = meta["H"], meta["NK"]
-        nqt = meta.get("QN") or meta.get("W", 2) * 32
-        split = meta.get("KVSPLIT", 0)
-        nkt = nk // 64
-        parts = [split or nkt] + ([nkt - split] if split else [])
-        geo = [(meta.get("KT") or parts[0], meta.get("K0", 0))]
-        if split:
-            geo.append((meta.get("PT") or parts[1], meta.get("P0", 0)))
-        q = decode_q(before[0], H, meta.get("QT") or nqt, meta.get("Q0", 0), nqt)
-        kvs = [decode_kv(b, H, t_all, t0, n) for b, (t_all, t0), n in zip(before[1:-1], geo, parts)]
-        k = np.concatenate([x[0] for x in kvs], 1)
-        v = np.concatenate([x[1] for x in kvs], 1)
-        ref = AT.attention_ref(q, k, v, nkv=meta.get("NKV") or nk)
-        rows_all, cols_all, h0, nrows = nqt * 64, meta.get("OHEADS", 32) * 128, meta.get("H0", 0), nqt * 64
+        nq = 64 * (meta.get("QN") or meta.get("W", 2) * 32)
+        q_all = decode_q(before[0], H, before[0].numel() // (H * TILE9), 0, before[0].numel() // (H * TILE9))
+        q0 = 64 * meta.get("Q0", 0)
+        assert q0 + nq <= q_all.shape[1]
+        q = q_all[:, q0:q0 + nq]
+        n1 = 64 * meta["KVSPLIT"] if meta.get("KVSPLIT") else nk
+        ranges = [(64 * meta.get("K0", 0), n1)] + ([(64 * meta.get("P0", 0), nk - n1)] if n1 < nk else [])
+        ks, vs = [], []
+        for buf, (r0, n) in zip(before[1:-1], ranges):
+            k_all, v_all = _kv_rows(buf, H)
+            assert r0 + n <= k_all.shape[1]
+            ks.append(k_all[:, r0:r0 + n])
+            vs.append(v_all[:, r0:r0 + n])
+        ref = AT.attention_ref(q, np.concatenate(ks, 1), np.concatenate(vs, 1), nkv=meta.get("NKV") or nk)
+        rows_all, cols_all, h0, nrows = nq, meta.get("OHEADS", 32) * 128, meta.get("H0", 0), nq
     heads = ref.shape[0]
     pos = F.a_pos(*np.meshgrid(np.arange(rows_all), np.arange(0, cols_all, 8), indexing="ij"), rows_all, cols_all)
     blk = (pos // 8).reshape(rows_all, cols_all // 8)

@@ -7,7 +7,7 @@
 // The packed stream is read once with coalesced 1 KB loads: a workgroup owns one 16-column group, which for every K
 // tile is 1152 contiguous bytes. Lanes re-read whole blocks (16 columns x 8 K) from LDS. The activation is quantized
 // to bfp16 blocks of 8 along K like the GEMM's A operand, so every block product is two int8 dot4 instructions and
-// one exact power-of-two scale. Lane sums are reduced with a transposing butterfly, the two waves' K halves in LDS.
+// one exact power-of-two scale. Lane sums are reduced with a transposing butterfly, then the three waves' K parts in LDS.
 #include "rlbfp.h"
 #include "rlbfp_device.h"
 #include "rlbfp_host.h"
@@ -29,13 +29,14 @@ __device__ __forceinline__ float silu_v(float x) {
 
 // Workgroup = one 16-column group g of the b_layout (N tile g / 8, super-block g % 8), all of K. Wave w of 3 takes
 // the iterations it = w, w + 3, ... of 8 K tiles each (2 per wave at K = 3072: 3456 waves, at most 4 per SIMD, all
-// resident with 112 VGPRs). An iteration's 8 x 1152 bytes are read with 9 coalesced 1 KB
-// loads; they pass through the wave's own 9 KB of LDS, from which lane l = (run, br) = (l/8, l%8) reads its 16 blocks
-// (K rows br*8..+7 of K tile 8 it + run, 16 columns) as 144 aligned bytes at offset 144 l (a 36-dword stride, which
-// covers all banks). Iterations go in groups of two whose loads are issued at once (the first straight into LDS, the
-// other into registers), which is all of a wave's 18 KB at K = 3072, and act(x) for both is quantized while the
-// blocks are in flight: the math left behind the last bytes to arrive is the block products of at most two
-// iterations. (Two waves of three iterations each took 5% longer: more math behind the last bytes per wave.)
+// resident). An iteration's 8 x 1152 bytes are read with 9 coalesced 1 KB direct-to-LDS
+// loads into the wave's own 9 KB of LDS, from which lane l = (run, br) = (l/8, l%8) reads its 16 blocks (K rows
+// br*8..+7 of K tile 8 it + run, 16 columns) as 144 aligned bytes at offset 144 l (a 36-dword stride, which covers
+// all banks). The next iteration's loads go into the same buffer as soon as the lanes' reads of the current one have
+// returned, before its block products: so no iteration is staged through registers, and the math left behind the
+// last bytes to arrive is one iteration's block products. act(x) of a pair of iterations is quantized while the
+// first one's blocks are in flight. (The previous form, the second iteration loaded into registers at once and staged
+// through LDS after the first, measured 1-3% slower with the same bits; two waves of three iterations each 5% slower.)
 //
 // act(x) of the lane's 8 K rows is quantized to one bfp16 block per row of x (E = largest float32 exponent field,
 // q = rint(v * 2^(133-E)) clipped to [-128, 127], as the activation encoder does), so that each weight block
@@ -44,7 +45,6 @@ template <int M, bool SILU>
 __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ B, uint16_t* __restrict__ y,
     int64_t ldy, int32_t N, int32_t K) {
-  constexpr int S = 1;  // register slots: with the LDS slot, a group of two iterations in flight
   __shared__ __attribute__((aligned(16))) uint8_t buf[kVWaves][kVIterBytes];
   __shared__ float red[kVWaves][M][16];
   // the wave index is uniform across the wave: readfirstlane puts it (and the load offsets built from it) in scalar
@@ -67,18 +67,12 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
     const int ci = 64 * i + lane;
     voff[i] = (uint32_t)(((int64_t)nt * KT + ci / 72) * 9216 + sbc * 1152 + 16 * (ci % 72));
   }
-  u32x4 w[S][9], xs[S][M], x0[M];
+  u32x4 x1[M], x0[M];
   // x rows of iteration idx (M loads, unconditional: past the last K tile they read the clamped tile)
   auto xload = [&](int idx, u32x4 (&dx)[M]) {
     const int kt = min(8 * (wave + kVWaves * idx) + run, KT - 1);
 #pragma unroll
     for (int m = 0; m < M; m++) dx[m] = *reinterpret_cast<const u32x4*>(x + m * ldx + kt * 64 + br * 8);
-  };
-  auto wload = [&](int idx, u32x4 (&dw)[9]) {
-    const int it = wave + kVWaves * idx;
-#pragma unroll
-    for (int i = 0; i < 9; i++)
-      dw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[i], it * 8 * 9216, kLoadStream));
   };
   // iteration 0 goes straight to the wave's LDS buffer (lane l of load i lands at 1024 i + 16 l, the staged order)
   auto dma = [&](int idx) {
@@ -95,11 +89,6 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
 #pragma unroll
     for (int j = 0; j < 16; j++) part[m][j] = 0.f;
 
-  // realign through LDS: the coalesced chunks go in as loaded, each lane takes out its 144-byte run of blocks
-  auto stage = [&](const u32x4 (&dw)[9]) {
-#pragma unroll
-    for (int i = 0; i < 9; i++) *reinterpret_cast<u32x4*>(&buf[wave][1024 * i + 16 * lane]) = dw[i];
-  };
   // act(x) of iteration idx's 8 K rows, quantized to one bfp16 block per row of x. Past the last K tile (whose
   // blocks may be the next N tile's) the x block is zero, so those products are exactly 0 and the block loop runs
   // without a branch.
@@ -130,12 +119,14 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
       if (kt >= KT) o.q[m][0] = o.q[m][1] = 0u;
     }
   };
-  auto body = [&](const XQ& xq) {
-    const auto& qx = xq.q;
-    const auto& ex = xq.e;
-    u32x4 cur[9];
+  // the lane's 144-byte run of the iteration in the wave's buffer
+  auto rd = [&](u32x4 (&cur)[9]) {
 #pragma unroll
     for (int i = 0; i < 9; i++) cur[i] = *reinterpret_cast<const u32x4*>(&buf[wave][144 * lane + 16 * i]);
+  };
+  auto body = [&](const XQ& xq, const u32x4 (&cur)[9]) {
+    const auto& qx = xq.q;
+    const auto& ex = xq.e;
     {
       const uint32_t* wd = reinterpret_cast<const uint32_t*>(cur);
 #pragma unroll
@@ -155,46 +146,45 @@ __global__ __launch_bounds__(kVThreads, M == 1 ? 4 : (M <= 3 ? 2 : 1)) void gemv
     }
   };
 
-  // Iterations go in groups of 1 + S, all requested at once: the first into LDS, the others into the register
-  // slots. A group is straight-line code, so each wait is for its own iteration only (with uses under a branch the
-  // compiler would sink the loads into it). Loads past this wave's iterations are safe: buffer loads beyond the
-  // stream return zeros, x loads use a clamped K tile.
-  for (int g0 = 0; g0 < mine; g0 += 1 + S) {
-    // issue order (fenced, and the waits below count on it): the group's x rows, then the blocks of the first
-    // iteration (into LDS), then those of the others
+  // Iterations go in pairs: the x rows of both, then the first one's blocks straight into the wave's LDS buffer; the
+  // second's go into the same buffer once the lanes' reads of the first have returned, and the first one's block
+  // products run while they are in flight. A pair is straight-line code, so each wait counts exactly (with uses under
+  // a branch the compiler would sink the loads into it). Loads past this wave's iterations are safe: buffer loads
+  // beyond the stream return zeros, x loads use a clamped K tile, and their x blocks are zero.
+  for (int g0 = 0; g0 < mine; g0 += 2) {
+    // issue order (fenced, and the waits below count on it): the pair's x rows, then the first iteration's blocks
     xload(g0, x0);
-#pragma unroll
-    for (int s0 = 0; s0 < S; s0++) xload(g0 + 1 + s0, xs[s0]);
+    xload(g0 + 1, x1);
     __builtin_amdgcn_sched_barrier(0);
     dma(g0);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s0 = 0; s0 < S; s0++) {
-      wload(g0 + 1 + s0, w[s0]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // the x rows land first: for up to 4 rows of x, act(x) of all the group's iterations is quantized while the blocks
-    // are still in flight (more rows would not fit the registers; they are quantized per iteration)
+    // the x rows land first: for up to 4 rows of x, act(x) of both iterations is quantized while the blocks are still
+    // in flight (more rows would not fit the registers; they are quantized per iteration)
     constexpr bool kEarly = M <= 4;
-    XQ xq[1 + S];
+    XQ xq[2];
     if constexpr (kEarly) {
-      wait_vm<9 * (1 + S)>();
+      wait_vm<9>();
       quant(g0, x0, xq[0]);
-#pragma unroll
-      for (int s0 = 0; s0 < S; s0++) quant(g0 + 1 + s0, xs[s0], xq[1 + s0]);
+      quant(g0 + 1, x1, xq[1]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    wait_vm<9 * S>();  // the group's first iteration has landed
+    wait_vm<0>();  // the first iteration has landed
     if constexpr (!kEarly) quant(g0, x0, xq[0]);
-    body(xq[0]);
+    u32x4 cur[9];
+    rd(cur);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the reads have returned, the buffer is free
+    __builtin_amdgcn_sched_barrier(0);
+    dma(g0 + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    body(xq[0], cur);
+    __builtin_amdgcn_sched_barrier(0);  // the first iteration's math before the second one's wait
     // iterations past this wave's last one have every K tile >= KT, so their x blocks are zero and they add 0
-#pragma unroll
-    for (int s0 = 0; s0 < S; s0++) {
-      __builtin_amdgcn_sched_barrier(0);  // one iteration's math before the next one's wait
-      stage(w[s0]);
-      if constexpr (!kEarly) quant(g0 + 1 + s0, xs[s0], xq[1 + s0]);
-      body(xq[1 + s0]);
-    }
+    wait_vm<0>();
+    if constexpr (!kEarly) quant(g0 + 1, x1, xq[1]);
+    rd(cur);
+    body(xq[1], cur);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the reads are done before the next pair's loads rewrite the buffer
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // reduce over the 64 lanes (run: lane bits 5..3, br: bits 2..0) with a transposing butterfly over bits 5..2

@@ -865,9 +865,15 @@ __device__ __forceinline__ void ep4_partial(const GemmDesc& d, const float* ep, 
   }
 }
 
-template <int G, int MF, bool kOut>
+// kReg: the variant for a SwiGLU GEMM with no bias, gate or residual, whole K, into a row-major bf16 C (the FFN up
+// GEMMs). Its MFMAs take B as the first operand and A as the second, which gives the transposed accumulator tile
+// with the same sums: lane l then holds row l % 16, columns 4 (l / 16) .. + 3 of each 16 x 16 fragment, so the
+// gate and proj values of one output sit in one lane, and an output block of 8 columns in lanes l and l ^ 16. The
+// epilogue runs from those registers (no LDS tile, no barrier).
+template <int G, int MF, bool kOut, bool kReg = false>
 __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G> args) {
   static_assert(MF >= 4 && MF <= 8, "four decode octets per phase, 8 x 8 accumulators at most");
+  static_assert(!kReg || (G == 1 && !kOut), "the register epilogue serves one row-major GEMM");
   constexpr int TM = 64 * MF;       // tile rows: 16 MF per wave, four waves down
   constexpr int kAS = TM * BK * 2;  // bytes of one A stage
   constexpr int kDma = TM / 32;     // A loads of 8 rows per wave per stage
@@ -1004,7 +1010,10 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mf], cur[j], acc[mf][j], 0, 0, 0);
+        if constexpr (kReg)
+          acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cur[j], fa[mf], acc[mf][j], 0, 0, 0);
+        else
+          acc[mf][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mf], cur[j], acc[mf][j], 0, 0, 0);
         if (j == 1) nxt[mf] = read_b(nb, mf);
         if (mf == MF - 1 && j >= 2 && MF + j - 2 < 8) nxt[MF + j - 2] = read_b(nb, MF + j - 2);
       }
@@ -1051,6 +1060,68 @@ __global__ __launch_bounds__(kW4Threads, 1) void gemm4w_kernel(const GemmArgs<G>
     phase.template operator()<1>(fb1, fb0, lds + s1 * kAS + aoff0, bl + s1 * kW4BStage + boff, nullptr, kl, s0);
   }
   wait_vm<0>();
+  if constexpr (kReg) {
+    // SwiGLU of the gate group g and the proj group g + 4 of one row fragment (16 outputs per lane) at a time, each
+    // step of silu_f over all 16 so that independent exp2 / reciprocal latencies overlap (per output the operations
+    // and their order are silu_f's), then bf16 rounding. Lane l = 16 k + r holds columns 4 k .. 4 k + 3 of each
+    // group; one row swap (permlane16_swap: lanes of odd k trade with lanes of k - 1) per word of a group pair
+    // (g0, g1) leaves lanes of even k with the 8-column block of g0 at columns 8 (k / 2) .., odd k with that of g1.
+    // Each lane then re-quantizes (RL_EP_QUANTIZE_OUT) and stores whole blocks, as finish_rows4 does: the float
+    // fast path when every block of the wave allows it, else the integer encoder for all (the same bits wherever
+    // the fast path applies). The four lanes of a row store 64 contiguous bytes per group pair.
+    const bool quant = (d.flags & RL_EP_QUANTIZE_OUT) != 0;
+    const int k = lane >> 4;
+    const int row0 = m0 + 16 * MF * wave + (lane & 15);
+    uint16_t* const c0 = d.C + (int64_t)row0 * d.ldc + n0 / 2 + 16 * (k & 1) + 8 * (k >> 1);
+#pragma unroll
+    for (int mf = 0; mf < MF; mf++) {
+      __builtin_amdgcn_sched_barrier(0);  // one row fragment at a time (interleaving them all runs out of registers)
+      float x[16], u[16], e[16];
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          x[4 * g + i] = acc[mf][g][i];
+          u[4 * g + i] = acc[mf][g + 4][i];
+        }
+#pragma unroll
+      for (int t = 0; t < 16; t++) e[t] = -1.4426950408889634f * x[t];
+#pragma unroll
+      for (int t = 0; t < 16; t++) e[t] = __builtin_amdgcn_exp2f(e[t]);
+#pragma unroll
+      for (int t = 0; t < 16; t++) e[t] = 1.0f + e[t];
+#pragma unroll
+      for (int t = 0; t < 16; t++) e[t] = __builtin_amdgcn_rcpf(e[t]);
+#pragma unroll
+      for (int t = 0; t < 16; t++) e[t] = (x[t] * e[t]) * u[t];
+      uint32_t w[8];  // w[2 g + h]: columns 4 k + 2 h, + 1 of group g
+#pragma unroll
+      for (int t = 0; t < 8; t++) w[t] = pack_bf16_rne(e[2 * t], e[2 * t + 1]);
+      u32x4 o[2];  // block of group 2 p + (k & 1), columns 8 (k >> 1) .. + 7
+#pragma unroll
+      for (int p = 0; p < 2; p++) {
+        const auto r0 = __builtin_amdgcn_permlane16_swap(w[4 * p], w[4 * p + 2], false, false);
+        const auto r1 = __builtin_amdgcn_permlane16_swap(w[4 * p + 1], w[4 * p + 3], false, false);
+        o[p] = u32x4{(uint32_t)r0[0], (uint32_t)r1[0], (uint32_t)r0[1], (uint32_t)r1[1]};
+      }
+      if (quant) {
+        const uint32_t E0 = block_exp8(o[0]), E1 = block_exp8(o[1]);
+        const bool slow = E0 < kFastEMin || E0 > kFastEMax || E1 < kFastEMin || E1 > kFastEMax;
+        if (__builtin_amdgcn_ballot_w64(slow) == 0) {
+          o[0] = requantize8_fast(o[0], E0);
+          o[1] = requantize8_fast(o[1], E1);
+        } else {
+          o[0] = quantize_bf16x8(o[0]);
+          o[1] = quantize_bf16x8(o[1]);
+        }
+      }
+      if (row0 + 16 * mf < d.M) {
+        *reinterpret_cast<u32x4*>(c0 + 16 * mf * d.ldc) = o[0];
+        *reinterpret_cast<u32x4*>(c0 + 16 * mf * d.ldc + 32) = o[1];
+      }
+    }
+    return;
+  }
   __syncthreads();
 
   // ---- epilogue: bias and activation (SwiGLU: silu(gate) * proj of groups g and g + 4) in registers, fp32 results
@@ -1415,8 +1486,27 @@ static int launch4w_v(const GemmArgs<G>& args, int total_tiles, int mf, void* st
   }
   return launch_status("rl_bfp16_gemm");
 }
+// The register-epilogue variant (gemm4w_kernel's kReg) serves a SwiGLU GEMM of whole K with no bias, gate or
+// residual, into a row-major bf16 C only.
+static bool wants_reg_variant(const GemmDesc& g) {
+  return g.act == RL_ACT_SWIGLU && g.ksplit == 1 && !g.bias && !g.gate && !g.res && !g.pk && !g.c_atb && g.C;
+}
+static int launch4w_reg(const GemmArgs<1>& args, int total_tiles, int mf, void* stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(total_tiles), block(kW4Threads);
+  switch (mf) {
+    case 8: hipLaunchKernelGGL((gemm4w_kernel<1, 8, false, true>), grid, block, 0, st, args); break;
+    case 7: hipLaunchKernelGGL((gemm4w_kernel<1, 7, false, true>), grid, block, 0, st, args); break;
+    case 6: hipLaunchKernelGGL((gemm4w_kernel<1, 6, false, true>), grid, block, 0, st, args); break;
+    default: hipLaunchKernelGGL((gemm4w_kernel<1, 4, false, true>), grid, block, 0, st, args); break;
+  }
+  return launch_status("rl_bfp16_gemm");
+}
 template <int G>
 static int launch4w(const GemmArgs<G>& args, int total_tiles, int mf, void* stream) {
+  if constexpr (G == 1) {
+    if (wants_reg_variant(args.d[0])) return launch4w_reg(args, total_tiles, mf, stream);
+  }
   return wants_out_variant(args) ? launch4w_v<G, true>(args, total_tiles, mf, stream)
                                  : launch4w_v<G, false>(args, total_tiles, mf, stream);
 }

@@ -10,7 +10,8 @@ captured once as a HIP graph and replayed (its eager time, launched from Python,
 roofline object is for the dominant kernel, the up GEMM (657.13 GFLOP per call), against the dense bf16 MFMA peak; the
 library runs that call as two launches (the 4-wave kernel over rows 0..4095 in 512 x 128 tiles, six full rounds of the
 256 CUs, then the same kernel over the last 256 rows in 256 x 128 tiles), timed together. Kernel times are medians of
-HIP-event intervals on the launch stream.
+HIP-event intervals on the launch stream. Before the warmup steps the step runs untimed for SETTLE_S seconds, so that
+the timed steps see the sustained clock rather than power management's first tens of milliseconds.
 Also reported: the adaLN modulation GEMV (M=1, K=3072, N=18432, SiLU) in GB/s against HBM (8 TB/s), timed over six
 rotating weight copies so that the 256 MB MALL cannot hold them; the residual + LayerNorm + modulate pass that
 produces the up GEMM's A (4352 x 3072) and the QKV post pass (4352 tokens x 24 heads) in GB/s against HBM; attention
@@ -36,9 +37,10 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA (vendor figure)
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 # HBM bytes per up-GEMM call (its two launches) from rocprofv3 FETCH_SIZE (x2) and WRITE_SIZE (x1), the factors that make a 256 MB
 # device-to-device copy read and write 256 MB (profiles/gemm_dit_ffn_counters.md); re-measured when the kernel changes
-UP_GEMM_TRAFFIC_BYTES = 846841373
+UP_GEMM_TRAFFIC_BYTES = 853128984
 M, K, FF = 4352, 3072, 12288
 GEMV_K, GEMV_N = 3072, 18432
+SETTLE_S = 0.3  # seconds of untimed steps before the warmup steps (the clock settles within ~50 ms of load)
 
 
 def flops_up():
@@ -122,6 +124,7 @@ def gpu_bench(steps, warmup, no_configs=False):
         if tm:
             tm.mark("end")
 
+    settle(step)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -145,6 +148,7 @@ def gpu_bench(steps, warmup, no_configs=False):
         with torch.cuda.graph(graph, stream=side):
             step()
     torch.cuda.current_stream().wait_stream(side)
+    settle(graph.replay)
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -210,6 +214,7 @@ def gpu_bench(steps, warmup, no_configs=False):
     torch.cuda.synchronize()
     ref = ops.gemv(rng_x, copies[(per_graph - 1) % 6], GEMV_N)
     assert torch.equal(ref, ym), "graph replay of the GEMV differs from the eager result"
+    settle(graph.replay)
     reps = 4
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -313,6 +318,7 @@ def graph_us(call, warm, per_graph, reps):
     torch.cuda.current_stream().wait_stream(side)
     graph.replay()
     torch.cuda.synchronize()
+    settle(graph.replay)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -320,6 +326,24 @@ def graph_us(call, warm, per_graph, reps):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def settle(run, seconds=None):
+    """Runs `run()` untimed for SETTLE_S seconds (a synchronisation every tenth call) right before a timed region.
+    On an MI355X that was idle, even for a few ms of host work between two timed regions, power management takes some
+    tens of ms of load to settle the clock: the first ~50 FFN steps from cold run the up GEMM at ~537 us, then
+    518-522 us for seconds on the same box, and a step graph replayed right after host work measured 8% slower than
+    the settled eager steps before it."""
+    import torch
+
+    t = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t < (SETTLE_S if seconds is None else seconds):
+        run()
+        n += 1
+        if n % 10 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
 
 
 def attn_bench(dev, heads=24, per_graph=10, reps=3):
@@ -344,7 +368,7 @@ def attn_bench(dev, heads=24, per_graph=10, reps=3):
     f = torch.nn.functional.scaled_dot_product_attention
     for _ in range(3):
         f(qs, ks, vs)
-    torch.cuda.synchronize()
+    settle(lambda: f(qs, ks, vs))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(per_graph):
@@ -717,7 +741,7 @@ def main():
         "metric": "bfp16-weight GEMM TFLOP/s and % bf16 MFMA peak at DiT FFN shape; GEMV GB/s",
         "value": round(step_flops / (ms_step * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "settle_s": SETTLE_S,
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_eager": round(r["ms_step_eager"], 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -727,7 +751,7 @@ def main():
                    "weights": "bfp16ebs8 ~N(0,0.02)", "activations": "bf16 ~N(0,1)", "seed": 0},
         "roofline": {"bound": "mfma", "achieved": round(up_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(up_tflops / PEAK_BF16_TFLOPS, 4), "traffic": UP_GEMM_TRAFFIC_BYTES,
-                     "kernel": "up GEMM 4352x3072x24576 + SwiGLU: gemm4w_kernel<1,8> rows 0..4095 + gemm4w_kernel<1,4> rows 4096..4351",
+                     "kernel": "up GEMM 4352x3072x24576 + SwiGLU: gemm4w_kernel<1,8,false,true> rows 0..4095 + gemm4w_kernel<1,4,false,true> rows 4096..4351 (register epilogue)",
                      "us": round(r["ms_up"] * 1e3, 2)},
         "kernels": {
             # the kernel alone (graph replays); algorithmic bytes: bf16 read + packed written (the pass also writes

@@ -107,6 +107,47 @@ def test_swiglu_interleaved(dev):
         check(out, G.gemm_ref(Aq, Bq, act=G.ACT_SWIGLU, **kw))
 
 
+@pytest.mark.parametrize("M,K,N,quant,scale", [
+    (300, 128, 2 * 256, False, 1.0),        # rows past M in the last tile
+    (1000, 256, 2 * 1024, True, 1.0),       # re-quantized output
+    (512, 128, 2 * 512, True, 2.0 ** 62),   # output blocks past the float fast path (E > 237: the integer encoder)
+])
+def test_register_epilogue_matches_staged(dev, M, K, N, quant, scale):
+    """The FFN up GEMMs (SwiGLU without bias, gate or residual, row-major C) run the 4-wave kernel's register epilogue
+    (transposed accumulators, 8-column blocks assembled by row swaps); a zero bias sends the same GEMM through the
+    LDS-staged epilogue (acc + 0 is acc bit for bit: an MFMA sum started from +0 is never -0). Bit-identical, and both
+    against the emulation."""
+    rng = np.random.default_rng(M + N)
+    A = G.activations(rng, M, K) * np.float32(scale)
+    Fh = N // 2
+    packed = F.pack_b(F.interleave_up(G.linear_weight(rng, Fh, K), G.linear_weight(rng, Fh, K)))
+    Aq = F.quantize_rows(A)
+    a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)
+    reg = ops.gemm(a, b, N, K, act="swiglu", quantize_out=quant)
+    staged = ops.gemm(a, b, N, K, act="swiglu", quantize_out=quant, bias=torch.zeros(N, device="cuda"))
+    assert torch.equal(reg, staged)
+    assert torch.isfinite(reg.float()).all()
+    if scale == 1.0:
+        check(reg, G.gemm_ref(Aq, F.decode_b(packed, K, N), act=G.ACT_SWIGLU, quantize_out=quant), tol=2e-2)
+    else:
+        o = reg.float().cpu().numpy()
+        assert np.abs(o).max() >= 2.0 ** 111  # the blocks the integer encoder serves
+        assert (F.quantize_rows(o) == o).mean() > 0.999
+
+
+def test_register_epilogue_ffn_up_full(dev):
+    """The FFN up GEMM at full size (4352 x 3072 x 2 x 12288: 512-row tiles over rows 0..4095, then 256-row tiles)
+    through the register epilogue, bit-identical to the LDS-staged one (zero bias)."""
+    M, K, N = 4352, 3072, 2 * 12288
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x = ops.quantize(torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16), deq=True)[1]
+    w = ops.pack_weight(ops.interleave_up(torch.randn((N // 2, K), generator=g, device="cuda") * 0.02,
+                                          torch.randn((N // 2, K), generator=g, device="cuda") * 0.02).contiguous())
+    reg = ops.gemm(x, w, N, K, act="swiglu", quantize_out=True)
+    staged = ops.gemm(x, w, N, K, act="swiglu", quantize_out=True, bias=torch.zeros(N, device="cuda"))
+    assert torch.equal(reg, staged)
+
+
 def test_gate_residual_split(dev):
     M, K, N = 384, 256, 256
     rng, A, packed, Aq, Bq = setup(M, K, N, 7)

@@ -217,6 +217,28 @@ def test_grouped_matches_single(dev):
         assert torch.equal(o, r)
 
 
+def test_grouped_deep_k_four_wave(dev):
+    """Members of K >= 8192 run as one launch of the 4-wave kernel (config 5's down projection): bit-identical to each
+    member's own whole-K launch, and against the emulation."""
+    rng = np.random.default_rng(12)
+    specs, refs, emu = [], [], []
+    for M, K, N, act in ((512, 8192, 384, None), (256, 8192, 256, "swiglu"), (100, 8192, 128, None)):
+        A = G.activations(rng, M, K)
+        if act:
+            packed = F.pack_b(F.interleave_up(G.linear_weight(rng, N // 2, K), G.linear_weight(rng, N // 2, K)))
+        else:
+            packed = F.pack_b(G.linear_weight(rng, N, K).T)
+        Aq = F.quantize_rows(A)
+        a, b = dev_t(Aq, torch.bfloat16), dev_t(packed, torch.uint8)
+        specs.append(ops.GemmSpec(a, b, N, K, act=act))
+        refs.append(ops.gemm(a, b, N, K, act=act, split=False))
+        emu.append(G.gemm_ref(Aq, F.decode_b(packed, K, N), act=G.ACT_SWIGLU if act else G.ACT_NONE))
+    outs = ops.gemm_grouped(specs)
+    for o, r, e in zip(outs, refs, emu):
+        assert torch.equal(o, r)
+        check(o, e)
+
+
 @pytest.mark.parametrize("a_fmt", ["packed_a_layout", "bf16_quantize"])
 def test_grouped_non_bf16_a(dev, a_fmt):
     """A grouped launch with A in another format (every member's A staged as bf16 in one allocation first) gives the

@@ -1771,9 +1771,9 @@ int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, v
   // one 8-wave launch for the whole group, with the fragment count that minimises its rounds; or, when the model
   // puts it lower, each member as its own planned launches (e.g. the SwiGLU up GEMMs of the image and text streams:
   // the 4-wave kernel's 512-row tiles over the 4096 image rows and 256-row tiles over the 256 text rows, where one
-  // launch would round both to 256-row tiles of the 8-wave kernel). At K = 3072 the 4-wave kernel's single launch
-  // measured slower than the 8-wave one (627-646 against 619 us for the two up GEMMs, 299-306 against 280 us for the
-  // two QKV GEMMs); for deep K it is faster (below).
+  // launch would round both to 256-row tiles of the 8-wave kernel). The 4-wave kernel is not used for the single
+  // launch: with members of different weights it measured slower than the 8-wave one (627-646 against 619 us for
+  // the two up GEMMs, 299-306 against 280 us for the two QKV GEMMs).
   const int cus = device_cus();
   int best_mf = 8;
   double bc = 1e300;
@@ -1789,26 +1789,6 @@ int rl_bfp16_gemm_grouped(const rl_gemm_desc* descs, int32_t n, int32_t a_fmt, v
     double c = 0;
     plans[i] = plan_gemm(args.d[i].M, args.d[i].N, cus, args.d[i].act, &c);
     each += c;
-  }
-  // Deep K (every member K >= 8192): one launch of the 4-wave kernel when the model puts it at or below the
-  // per-member launches. Its cheaper K steps then outweigh the 8-wave kernel's finer rounding of the group into tiles
-  // (config 5's down projection, (4096 + 256) x 12288 x 3072: 263 against 315 us, same bits; at K = 3072 the 8-wave
-  // launch stays ahead: its QKV 228 against 252 us).
-  int64_t kmin = INT64_MAX;
-  for (int i = 0; i < n; i++) kmin = min(kmin, (int64_t)args.d[i].K);
-  if (kmin >= 8192 && kernel_restriction() != 2) {
-    int mf4 = 0;
-    double c4 = 1e300;
-    for (int mf : kMf4Choices) {
-      int64_t t = 0;
-      for (int i = 0; i < n; i++) t += tiles4(args.d[i].M, args.d[i].N, mf);
-      const double c = launch_cost4(t, mf, cus);
-      if (c < c4) { c4 = c; mf4 = mf; }
-    }
-    if (c4 <= each) {
-      set_tiles4w(args, mf4, total);
-      return launch4w<RL_MAX_GROUP>(args, total, mf4, stream);
-    }
   }
   if (each < bc) {
     for (int i = 0; i < n; i++)

@@ -217,9 +217,9 @@ def test_grouped_matches_single(dev):
         assert torch.equal(o, r)
 
 
-def test_grouped_deep_k_four_wave(dev):
-    """Members of K >= 8192 run as one launch of the 4-wave kernel (config 5's down projection): bit-identical to each
-    member's own whole-K launch, and against the emulation."""
+def test_grouped_deep_k(dev):
+    """A group of deep-K members (K = 8192, as config 5's down projection; a SwiGLU member among them): bit-identical
+    to each member's own whole-K launch, and against the emulation."""
     rng = np.random.default_rng(12)
     specs, refs, emu = [], [], []
     for M, K, N, act in ((512, 8192, 384, None), (256, 8192, 256, "swiglu"), (100, 8192, 128, None)):

@@ -40,7 +40,9 @@ PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 UP_GEMM_TRAFFIC_BYTES = 853128984
 M, K, FF = 4352, 3072, 12288
 GEMV_K, GEMV_N = 3072, 18432
-SETTLE_S = 0.3  # seconds of untimed steps before the warmup steps (the clock settles within ~50 ms of load)
+# seconds of untimed runs before each timed region (the clock settles within ~50 ms of load); RLBFP_BENCH_SETTLE_S
+# overrides it (0 for counter-collection runs, where every extra dispatch is profiled)
+SETTLE_S = float(os.environ.get("RLBFP_BENCH_SETTLE_S", "0.3"))
 
 
 def flops_up():

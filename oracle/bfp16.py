@@ -88,9 +88,10 @@ def to_bfp16(x, truncate=False):
 
 def from_bfp16(raw):
     """uint8 stream (9 bytes per block) -> flat float32 values ``q * 2^(E - 133)`` (redline/npu_layouts.py:90-94).
-    Every decoded value is exact in float32 and in bfloat16, except q = -128 with E = 254: -2^128 is beyond both
-    formats' range and decodes to -inf (the reference's float64 result would be finite; such a block only arises
-    from inputs within half a step of -float32 max)."""
+    Every decoded value is exact in float32 and in bfloat16, except where |q| * 2^(E - 133) >= 2^128: q = -128 with
+    E = 254, and |q| >= 64 with E = 255. Those are beyond both formats' range and decode to +-inf (the reference's
+    float64 result would be finite; the encoder writes such blocks only for inputs within half a step of -float32 max,
+    and for infinite inputs)."""
     blk = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, BLOCK_BYTES)
     q = blk[:, 1:].view(np.int8).astype(np.float32)
     scale = np.ldexp(np.float32(1.0), blk[:, :1].astype(np.int32) - 133).astype(np.float32)  # exact, >= 2^-133

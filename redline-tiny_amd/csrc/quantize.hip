@@ -4,9 +4,11 @@
 // (:11-47) and pack_weights.pack_b (redline/pack_weights.py:72-79); rl_bfp16_dequantize replaces from_bfp16 (:90-94)
 // composed with the inverse layouts.
 //
-// One thread per block, walking the OUTPUT stream in order, so that a workgroup's 256 blocks are 2304 contiguous
-// bytes: they are assembled in LDS and written with 16-byte stores. Each block's 8 source values are one contiguous
-// 16-byte (bf16) or 32-byte (fp32) read. HBM-bound: 2 (or 4) bytes read + 9/8 written per value.
+// The encoder takes one block per thread, walking the OUTPUT stream in order, so that a workgroup's 256 blocks are
+// 2304 contiguous bytes: they are assembled in LDS and written with 16-byte stores. Each block's 8 source values are
+// one contiguous 16-byte (bf16) or 32-byte (fp32) read (4 blocks per thread, the decoder's form below, measured 1-17%
+// slower for the encoder). The decoder takes 4 blocks per thread, 1024 per workgroup. HBM-bound: 2 (or 4) bytes read
+// + 9/8 written per value (+ 2 written for the encoder's decoded copy; 9/8 read and 2 or 4 written for the decoder).
 #include "rlbfp.h"
 #include "rlbfp_device.h"
 #include "rlbfp_host.h"
@@ -96,32 +98,63 @@ __global__ __launch_bounds__(kQThreads) void quantize_kernel(const void* __restr
   for (int i = full * 16 + threadIdx.x; i < bytes; i += kQThreads) dst[i] = stage[i];
 }
 
+// One decoded block (8 values, bf16 words) stored at row r, column block cb of the output.
 template <int ODT>
-__global__ __launch_bounds__(kQThreads) void dequantize_kernel(const uint8_t* __restrict__ packed, int32_t order,
-                                                               int64_t rows, int64_t cols, void* __restrict__ out) {
-  const int64_t nblocks = rows * cols / 8;
-  const int64_t ob = (int64_t)blockIdx.x * kQThreads + threadIdx.x;
-  if (ob >= nblocks) return;
-  int64_t r, cb;
-  block_source(order, ob, rows, cols, r, cb);
-  const Window w = load_window_safe(packed, ob, nblocks);
-  const uint32_t o = (uint32_t)(ob & 3);  // (9 * ob) % 4
-  const uint32_t lo = __builtin_amdgcn_alignbyte(w.w1, w.w0, o);
-  const uint32_t hi = __builtin_amdgcn_alignbyte(w.w2, w.w1, o);
-  const uint32_t E = lo & 0xFFu;
-  const int32_t q[8] = {(int8_t)(lo >> 8), (int8_t)(lo >> 16), (int8_t)(lo >> 24), (int8_t)hi,
-                        (int8_t)(hi >> 8), (int8_t)(hi >> 16), (int8_t)(hi >> 24), (int8_t)(w.w2 >> (8 * o))};
-  uint32_t b[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) b[i] = decode_bf16_bits(q[i], E);
+__device__ __forceinline__ void store_decoded(void* out, int64_t r, int64_t cb, int64_t cols, u32x4 v) {
   if (ODT == RL_DTYPE_BF16) {
-    u32x4 v;
-    v.x = b[0] | (b[1] << 16); v.y = b[2] | (b[3] << 16); v.z = b[4] | (b[5] << 16); v.w = b[6] | (b[7] << 16);
     *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + r * cols + cb * 8) = v;
   } else {
     u32x4* p = reinterpret_cast<u32x4*>(static_cast<float*>(out) + r * cols + cb * 8);
-    p[0] = u32x4{b[0] << 16, b[1] << 16, b[2] << 16, b[3] << 16};
-    p[1] = u32x4{b[4] << 16, b[5] << 16, b[6] << 16, b[7] << 16};
+    p[0] = u32x4{v.x << 16, v.x & 0xFFFF0000u, v.y << 16, v.y & 0xFFFF0000u};
+    p[1] = u32x4{v.z << 16, v.z & 0xFFFF0000u, v.w << 16, v.w & 0xFFFF0000u};
+  }
+}
+
+// Each thread decodes 4 blocks, so a wave keeps 2304 bytes of loads in flight (one block per thread kept 576, too
+// few to cover HBM latency: 3.7-3.9 TB/s at 4352 x 3072).
+//   Tiled orders: thread t takes blocks 4t .. 4t + 3, whose 36 bytes (dword aligned) are one run read with two 16-byte
+//   loads and one 4-byte load. They are rows r .. r + 3 of one 8-column block (the within-8 digit rib / col is the
+//   last), so store j of a wave writes 8 rows x 128 bytes.
+//   Row-block order: thread t takes blocks t, t + 256, t + 512, t + 768 (a 12-byte window each), so each store of a
+//   wave writes 1 KB contiguous.
+// Values are q * 2^(E - 133) in float32 (decode_window), as from_bfp16 computes them: exact, and +-inf where the
+// product overflows (E = 254, q = -128; E = 255, |q| >= 64).
+template <int ODT>
+__global__ __launch_bounds__(kQThreads) void dequantize_kernel(const uint8_t* __restrict__ packed, int32_t order,
+                                                               int64_t rows, int64_t cols, void* __restrict__ out) {
+  typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+  const int64_t nblocks = rows * cols / 8;
+  const int64_t g0 = (int64_t)blockIdx.x * (4 * kQThreads);
+  if (order == RL_ORDER_ROWBLOCK) {
+    const int64_t cblocks = cols / 8;
+    Window w[4] = {};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int64_t ob = g0 + threadIdx.x + j * kQThreads;
+      if (ob < nblocks) w[j] = load_window_safe(packed, ob, nblocks);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int64_t ob = g0 + threadIdx.x + j * kQThreads;
+      if (ob >= nblocks) break;
+      const int64_t r = ob / cblocks;
+      const u32x4 v = __builtin_bit_cast(u32x4, decode_window(w[j].w0, w[j].w1, w[j].w2, (uint32_t)(ob & 3)));
+      store_decoded<ODT>(out, r, ob - r * cblocks, cols, v);
+    }
+    return;
+  }
+  const int64_t ob0 = g0 + 4 * threadIdx.x;
+  if (ob0 >= nblocks) return;  // tiled streams hold a multiple of 1024 blocks: a thread's run is whole
+  const uint8_t* src = packed + 9 * ob0;
+  const u32x4 a = reinterpret_cast<const u32x4_a4*>(src)[0], b = reinterpret_cast<const u32x4_a4*>(src)[1];
+  const uint32_t w[9] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, reinterpret_cast<const uint32_t*>(src)[8]};
+  int64_t r, cb;
+  block_source(order, ob0, rows, cols, r, cb);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    // block j starts at byte 9 j of the run: dword 2 j, byte offset j
+    const u32x4 v = __builtin_bit_cast(u32x4, decode_window(w[2 * j], w[2 * j + 1], w[2 * j + 2], (uint32_t)j));
+    store_decoded<ODT>(out, r + j, cb, cols, v);
   }
 }
 
@@ -162,7 +195,7 @@ int rl_bfp16_dequantize(const uint8_t* packed, int32_t order, int64_t rows, int6
   if (((uintptr_t)packed % 4) || ((uintptr_t)out % 16)) return fail(RL_ERR_ALIGN, "packed 4-, out 16-byte aligned");
   if ((s = check_device())) return s;
   const int64_t nblocks = rows * cols / 8;
-  const dim3 grid((unsigned)((nblocks + kQThreads - 1) / kQThreads));
+  const dim3 grid((unsigned)((nblocks + 4 * kQThreads - 1) / (4 * kQThreads)));  // 4 blocks per thread
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (out_dtype == RL_DTYPE_BF16)
     hipLaunchKernelGGL(dequantize_kernel<RL_DTYPE_BF16>, grid, dim3(kQThreads), 0, st, packed, order, rows, cols, out);

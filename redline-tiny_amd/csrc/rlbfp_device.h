@@ -62,7 +62,8 @@ __device__ __forceinline__ int32_t encode_elem(uint32_t u, uint32_t E) {
 }
 
 // bf16 bit pattern of q * 2^(E-133), built with integers (exact for every E, including bf16 subnormal results).
-// q == 0 gives +0, as from_bfp16 does.
+// q == 0 gives +0, as from_bfp16 does; a product of 2^128 or more (E = 254 with q = -128, E = 255 with |q| >= 64)
+// gives +-inf, as from_bfp16's float32 product does.
 __device__ __forceinline__ uint32_t decode_bf16_bits(int32_t q, uint32_t E) {
   if (q == 0) return 0u;
   const uint32_t sign = q < 0 ? 0x8000u : 0u;
@@ -70,7 +71,9 @@ __device__ __forceinline__ uint32_t decode_bf16_bits(int32_t q, uint32_t E) {
   const int p = 31 - __clz(a);                      // leading one, 0..7
   const int be = p + (int)E - 6;                    // biased exponent of the result
   uint32_t bits;
-  if (be >= 1)
+  if (be >= 255)
+    bits = 0x7F80u;  // overflow: infinity
+  else if (be >= 1)
     bits = ((uint32_t)be << 7) | ((a << (7 - p)) & 0x7Fu);
   else
     bits = a << E;  // subnormal: value / 2^-133

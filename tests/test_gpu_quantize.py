@@ -82,10 +82,46 @@ def test_adversarial_blocks(dev, dtype):
     p, q = ops.quantize(to_dev(x, dtype), deq=True)
     np.testing.assert_array_equal(p.cpu().numpy(), C.to_bfp16(x))
     np.testing.assert_array_equal(p.cpu().numpy(), F.to_bfp16(x))
-    fin = np.isfinite(x).all(1)
-    np.testing.assert_array_equal(q.float().cpu().numpy()[fin], F.quantize_rows(x)[fin])
+    np.testing.assert_array_equal(q.float().cpu().numpy(), F.quantize_rows(x))   # the E = 255 row decodes to +-inf
     e7 = F.to_bfp16(x[-3:-2]).reshape(9)                                # the E = 7 row: q = [96, 0, 0, 1, -1, 1, 0, 0]
     assert e7[0] == 7 and list(e7[1:].view(np.int8)) == [96, 0, 0, 1, -1, 1, 0, 0]
+
+
+@pytest.mark.parametrize("order,R,Cc", [("rowblock", 3, 2728), ("rowblock", 1023, 8), ("rowblock", 5, 24),
+                                        ("a_layout", 256, 128), ("b_layout", 256, 128), ("c_atb", 512, 1024)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dequantize_every_exponent(dev, order, R, Cc, dtype):
+    """Arbitrary streams, as a packed file may hold them: every exponent byte 0..255 under random q bytes, and the
+    overflow edges (E = 254 with q = -128, E = 255 with q = +-64 / +-65 / 127 / -128), decoded as from_bfp16 decodes
+    them: float32 products, subnormal for small E and +-inf where q * 2^(E - 133) >= 2^128. Both CPU decoders agree
+    first. Ragged streams (3 x 2728: 1023 blocks; 1023 x 8; 5 x 24: 15 blocks) end inside a thread's run of 4."""
+    rng = np.random.default_rng(R + Cc)
+    nb = R * Cc // 8
+    raw = rng.integers(0, 256, (nb, 9), dtype=np.uint8)
+    raw[:, 0] = np.arange(nb) % 256
+    edges = [(254, [-128, 127, -127, 64, -64, 65, -65, 1]), (255, [-128, 127, -127, 64, -64, 65, -65, 0]),
+             (0, [1, -1, -128, 127, 0, 2, -2, 3]), (6, [1, -1, -128, 127, 0, 2, -2, 3])]
+    for i, (e, q) in enumerate(edges):
+        if i < nb:
+            raw[i, 0] = e
+            raw[i, 1:] = np.array(q, np.int8).view(np.uint8)
+    flat = F.from_bfp16(raw.reshape(-1))
+    np.testing.assert_array_equal(flat.view(np.uint32), C.from_bfp16(raw.reshape(-1)).view(np.uint32))
+    assert np.isinf(flat).any() and ((np.abs(flat) < 2.0**-126) & (flat != 0)).any()
+    if order == "rowblock":
+        want = flat.reshape(R, Cc)
+    elif order == "a_layout":
+        want = F.a_unlayout(flat, R, Cc)
+    elif order == "b_layout":
+        want = F.b_unlayout(flat, Cc, R).T     # the decoded matrix is W (N rows, K columns)
+    else:
+        want = F.c_unlayout_atb(flat, R, Cc)
+    got = ops.dequantize(to_dev(raw.reshape(-1), torch.uint8), R, Cc, order=order, dtype=dtype)
+    if dtype == torch.bfloat16:
+        np.testing.assert_array_equal(got.view(torch.int16).cpu().numpy().view(np.uint16),
+                                      (np.ascontiguousarray(want).view(np.uint32) >> 16).astype(np.uint16))
+    else:
+        np.testing.assert_array_equal(got.cpu().numpy().view(np.uint32), np.ascontiguousarray(want).view(np.uint32))
 
 
 def test_truncate_variant_differs(dev):

@@ -39,6 +39,23 @@ def test_kat_decode(case):
     np.testing.assert_array_equal(C.from_bfp16(raw).astype(np.float64), want)
 
 
+def test_decode_every_exponent_byte():
+    """Arbitrary 9-byte blocks (every E byte 0..255, every q byte -128..127): both decoders give the float64 product
+    q * 2^(E - 133) wherever it is below 2^128 (all of them exact in float32, subnormal below 2^-126), and +-inf at and
+    above it (E = 254 with q = -128, E = 255 with |q| >= 64)."""
+    E, q = np.meshgrid(np.arange(256), np.arange(-128, 128), indexing="ij")
+    E, q = E.reshape(-1), q.reshape(-1)
+    n = E.size // 8
+    raw = np.zeros((n, 9), np.uint8)
+    raw[:, 0] = E.reshape(n, 8)[:, 0]                 # 8 consecutive q values share one E (E changes every 32 blocks)
+    raw[:, 1:] = q.reshape(n, 8).astype(np.int8).view(np.uint8)
+    exact = q.astype(np.float64) * np.ldexp(1.0, E - 133)
+    want = np.where(np.abs(exact) >= 2.0**128, np.copysign(np.inf, exact), exact)
+    for got in (F.from_bfp16(raw), C.from_bfp16(raw)):
+        np.testing.assert_array_equal(got.astype(np.float64), want)
+    assert np.isinf(want).sum() == 1 + 65 + 64 and (want[(E == 0) & (q == 1)] == 2.0**-133).all()
+
+
 def adversarial(rng, nblocks):
     """Blocks built to hit ties, saturation, -128, zeros, subnormals and wide exponent spreads."""
     out = []

@@ -262,8 +262,8 @@ __device__ __forceinline__ void store_block1(uint8_t* p, uint32_t E, const uint3
 // operands (the caller does not store them), and the re-quantize takes its float fast path for all four at once when
 // every lane's blocks allow it (a wave-uniform test): the rows' dependency chains then interleave, which a wave with
 // no other wave on its SIMD needs.
-__device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int ocol, int nout, float (&v)[4][8],
-                                             u32x4 (&o)[4]) {
+__device__ __forceinline__ void finish_rows4_bf16(const GemmDesc& d, int row0, int ocol, int nout, float (&v)[4][8],
+                                                  u32x4 (&o)[4]) {
   if (d.gate || d.res) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -287,6 +287,10 @@ __device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int oc
   for (int i = 0; i < 4; i++)
     o[i] = u32x4{pack_bf16_rne(v[i][0], v[i][1]), pack_bf16_rne(v[i][2], v[i][3]), pack_bf16_rne(v[i][4], v[i][5]),
                  pack_bf16_rne(v[i][6], v[i][7])};
+}
+__device__ __forceinline__ void finish_rows4(const GemmDesc& d, int row0, int ocol, int nout, float (&v)[4][8],
+                                             u32x4 (&o)[4]) {
+  finish_rows4_bf16(d, row0, ocol, nout, v, o);
   if (d.flags & RL_EP_QUANTIZE_OUT) {
     uint32_t E[4];
     bool slow = false;
@@ -369,19 +373,48 @@ __device__ __forceinline__ void ep8_finish(const GemmDesc& d, const float* ep, i
 #pragma unroll
     for (int k = 0; k < 8; k++) a[k] = *reinterpret_cast<const f32x4*>(ep + (q * W + ep_slot(8 * cb + k)) * 4);
     if (kOut && d.pk) {
-      // packed output, one row at a time (fewer live registers; the quad is inside M, checked above, and then all
-      // four rows are, M % 128 == 0): the four rows' blocks are 36 consecutive bytes of the packed order
+      // packed output, the four rows together (the quad is inside M, checked above, and then all four rows are,
+      // M % 128 == 0), as finish_block_pk does per row but with one wave-uniform test for the float fast path of all
+      // four blocks, so that their dependency chains interleave (1% faster than row by row); the four rows' blocks
+      // are 36 consecutive bytes of the packed order
+      float v4[4][8];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int k = 0; k < 8; k++) v4[i][k] = a[k][i];
+      u32x4 o4[4];
+      finish_rows4_bf16(d, row0, col, nout, v4, o4);
       uint32_t E[4], ql[4], qh[4];
+      bool slow = false;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        float v[8];
+        E[i] = block_exp8(o4[i]);
+        slow |= E[i] < kFastEMin || E[i] > kFastEMax;
+      }
+      const bool quant = (d.flags & RL_EP_QUANTIZE_OUT) != 0;
+      if (__builtin_amdgcn_ballot_w64(slow) == 0) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = a[k][i];
-        uint32_t qw[2];
-        const u32x4 o = finish_block_pk(d, row0 + i, col, nout, v, E[i], qw);
-        ql[i] = qw[0];
-        qh[i] = qw[1];
-        if (d.C) *reinterpret_cast<u32x4*>(c_block(d, row0 + i, col, nout)) = o;
+        for (int i = 0; i < 4; i++) {
+          uint32_t qw[2];
+          const u32x4 oq = requantize8_fast_q(o4[i], E[i], qw);
+          if (quant) o4[i] = oq;
+          ql[i] = qw[0];
+          qh[i] = qw[1];
+        }
+      } else {
+        // the integer encoder for all four blocks (it gives the fast path's bits wherever that applies)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          uint32_t qw[2];
+          const u32x4 oq = requantize8_int_q(o4[i], qw);
+          if (quant) o4[i] = oq;
+          ql[i] = qw[0];
+          qh[i] = qw[1];
+        }
+      }
+      if (d.C) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4*>(c_block(d, row0 + i, col, nout)) = o4[i];
       }
       store_blocks4(d.pk + 9 * out_block(d.pk_order, d.prow + row0, col, nout), E, ql, qh);
       continue;

@@ -164,3 +164,20 @@ def test_packed_tiles_past_m(dev, N):
     torch.cuda.synchronize()
     assert bool((flat[M * N:] == 5.0).all()), "elements past the ATB-ordered C were written"
     assert np.array_equal(flat[:M * N].float().cpu().numpy(), F.c_layout_atb(y.float().cpu().numpy()))
+
+
+def test_packed_qkv_full(dev):
+    """The DiT block's QKV GEMM at full size as the reference's op list runs it (M = 4608, K = 3072, N = 9216, the C
+    stream in the ATB order): the planner's two launches (4-wave tiles, then the 8-wave kernel past them) write the
+    same bytes as the quantize pass over the bf16 C, and a bf16 C written beside them equals the plain call's."""
+    M, K, N = 4608, 3072, 9216
+    g = torch.Generator(device="cuda").manual_seed(21)
+    x = ops.quantize(torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16), deq=True)[1]
+    w = ops.pack_weight(torch.randn((N, K), generator=g, device="cuda") * 0.02)
+    y = ops.gemm(x, w, N, K)
+    pk = torch.full((M * N // 8 * 9,), 0x5A, dtype=torch.uint8, device="cuda")
+    ops.gemm(x, w, N, K, packed_out=pk)
+    assert torch.equal(pk, ops.quantize(y, order="c_atb")[0])
+    pk2 = torch.empty_like(pk)
+    c = ops.gemm(x, w, N, K, packed_out=pk2, out=torch.empty_like(y))
+    assert torch.equal(c, y) and torch.equal(pk2, pk)
